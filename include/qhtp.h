@@ -1,0 +1,159 @@
+/*
+ * qhtp.h -- C ABI of libqhtp, the MI355X (gfx950) implementation of qcom_htp's two hot
+ * paths: the QNN-semantics quantized matmul family and the GDN/KDA triangular solve.
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  Every pointer named *_dev is device memory on the
+ *     current HIP device; everything else is host memory.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Run entry
+ *     points are stream-ordered and never synchronise the host.
+ *   - Run entry points allocate nothing.  qh_qmm_prepare allocates the prepared weight
+ *     state (device memory) once; qh_qmm_release frees it.
+ *   - Every entry point validates its arguments and returns a status; no entry point
+ *     returns QH_STATUS_OK for a shape it did not compute.  qh_last_error() gives a
+ *     human-readable reason for the last failure on the calling thread.
+ *   - No global mutable state is shared between calls except the per-thread error text;
+ *     prepared handles are read-only during runs, so concurrent runs on different
+ *     streams are safe.
+ */
+#ifndef QHTP_H_
+#define QHTP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Values 0..3 mirror HmStatus of the reference's prepared-run ABI
+ * (example/handwritten_hmx_matmul/include/handwritten_hmx_matmul.h:11-16). */
+typedef enum qh_status {
+  QH_STATUS_OK = 0,
+  QH_STATUS_INVALID_ARGUMENT = 1,
+  QH_STATUS_UNSUPPORTED = 2,
+  QH_STATUS_RUNTIME_ERROR = 3,
+  QH_STATUS_SHAPE_UNSUPPORTED = 4,
+} qh_status;
+
+/* Replaces hm_status_string (handwritten_hmx_matmul.h:52). */
+const char *qh_status_string(qh_status status);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *qh_last_error(void);
+
+/* Library version as 0xMMmmpp. */
+uint32_t qh_version(void);
+
+/* ------------------------------------------------------------------------------------ */
+/* Quantized matmul family                                                               */
+/* ------------------------------------------------------------------------------------ */
+
+/* Weight storage handed to qh_qmm_prepare (host memory, logical [N][K] order). */
+typedef enum qh_weight_format {
+  QH_WEIGHT_I8 = 0,      /* int8 codes in [-127, 127], per-output-channel scale            */
+  QH_WEIGHT_I4 = 1,      /* int4 codes in [-7, 7] (one per int8), per-output-channel scale */
+  QH_WEIGHT_I4_LPBQ = 2, /* int4 codes in [-7, 7] times a per-(channel, K-block) integer  */
+                         /* scale in [1, 16], under a per-output-channel scale             */
+} qh_weight_format;
+
+/*
+ * One quantized matmul  out[M,N] = requant( (act[M,K] - act_zp) @ W[N,K]^T + bias[N] ).
+ *
+ * Semantics are those of the reference's float-derived oracle
+ * (scripts/generate_qnn_matmul_python_cases.py:446-481):
+ *   x_deq = (act - act_zp) * act_scale                            (float64)
+ *   w_deq = fl32(w_int * weight_scale[n])                        (float32 product)
+ *   bias_deq = bias_q[n] * fl64(act_scale * weight_scale[n])
+ *   out = clip(rint((x_deq @ w_deq^T + bias_deq) / out_scale + out_zp), 0, 2^out_bits - 1)
+ * w_int is the int8/int4 code, or code * block scale for LPBQ.  Results are bit-exact
+ * to that definition; the integer accumulation is exact.
+ *
+ * Shapes: K % 32 == 0, N % 32 == 0, K <= 65536, N <= 2^20; M is given per run (any M >= 1).
+ * act_bits / out_bits: 8 (uint8) or 16 (uint16).  LPBQ blocks: 32 or 64 along K.
+ *
+ * Replaces the reference op-package kernels HmxU8I8ToU8MatMul / HmxU8I4ToU8MatMul /
+ * HmxU16I8ToU16MatMul / HmxU16I4ToU16MatMul and the LPBQ expand pre-op
+ * HmxW4LpbqExpandToI8 (example/qnn_hmx_matmul_{u8i8,w4a8,w8a16,w4a16,common}/src; registration
+ * at HmxU8I8ToU8MatMulOp.cpp:783-884), whose precompute step (:196-287) corresponds to
+ * qh_qmm_prepare and whose hot callback (:289-405) corresponds to qh_qmm_run.
+ */
+typedef struct qh_qmm_desc {
+  uint32_t k;
+  uint32_t n;
+  uint32_t act_bits;      /* 8 or 16 */
+  uint32_t out_bits;      /* 8 or 16 */
+  uint32_t weight_format; /* qh_weight_format */
+  uint32_t lpbq_block;    /* 32 or 64 for QH_WEIGHT_I4_LPBQ, ignored otherwise */
+  int32_t act_zp;         /* activation zero point, 0 <= act_zp < 2^act_bits */
+  int32_t out_zp;         /* output zero point, 0 <= out_zp < 2^out_bits */
+  double act_scale;       /* > 0 */
+  double out_scale;       /* > 0 */
+  const int8_t *weight_nk;         /* [N][K] int codes                                  */
+  const uint8_t *lpbq_block_scale; /* [N][K / lpbq_block] in [1, 16] (LPBQ only)         */
+  const float *weight_scale;       /* [N] per-output-channel scale, > 0                 */
+  const int32_t *bias_q;           /* [N] int32 bias codes at act_scale*weight_scale, or NULL */
+} qh_qmm_desc;
+
+typedef struct qh_qmm_prepared qh_qmm_prepared;
+
+/* Build the device-resident prepared state (weight tiles, epilogue constants).
+ * Synchronous; allocates device memory on the current device. */
+qh_status qh_qmm_prepare(const qh_qmm_desc *desc, qh_qmm_prepared **out);
+
+/* out_dev[M][N] (uint8 or uint16, row-major) from act_dev[M][K] (uint8 or uint16,
+ * row-major; the reference's [1, M/32, 32, K] activation is this layout).  Picks the
+ * MFMA GEMM for M > 16 and the streaming GEMV for M <= 16. */
+qh_status qh_qmm_run(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
+                     void *stream);
+
+/* Same as qh_qmm_run with the kernel path forced: 0 = automatic, 1 = GEMM, 2 = GEMV. */
+qh_status qh_qmm_run_path(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
+                          uint32_t path, void *stream);
+
+/* Exact int32/int64 accumulators acc[M][N] = sum_k (act - act_zp) * w_int, written as
+ * int64 (the integer-accumulator contract of scripts/reconstruct_hmx_u8_drain.py:10-16). */
+qh_status qh_qmm_accumulate(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, int64_t *acc_dev,
+                            void *stream);
+
+typedef struct qh_qmm_info {
+  uint32_t k, n, act_bits, out_bits, weight_format, lpbq_block;
+  uint64_t device_bytes;      /* device memory held by the prepared state */
+  uint64_t gemm_weight_bytes; /* bytes of the GEMM weight tiles */
+  uint64_t gemv_weight_bytes; /* bytes the GEMV streams per call (weights + scales) */
+} qh_qmm_info;
+
+qh_status qh_qmm_query(const qh_qmm_prepared *prep, qh_qmm_info *info);
+
+/* Frees the prepared state (synchronises the device first). NULL is accepted. */
+qh_status qh_qmm_release(qh_qmm_prepared *prep);
+
+/* ------------------------------------------------------------------------------------ */
+/* GDN / KDA triangular solve  T = (I - A)^-1, A strictly lower triangular per head      */
+/* ------------------------------------------------------------------------------------ */
+
+typedef enum qh_gdn_precision {
+  QH_GDN_FP32 = 0, /* fp32 diagonal solves and fp32 MFMA merges (rel. Frobenius <= 1e-4)   */
+  QH_GDN_BF16 = 1, /* fp32 diagonal solves, bf16 MFMA merges with fp32 accumulation        */
+} qh_gdn_precision;
+
+/* A_dev: float32 [heads][C][C] row-major, only the strictly lower triangle is read.
+ * T_dev: float32 [heads][C][C]; the full matrix is written (zeros above the diagonal).
+ * C % 16 == 0, 16 <= C <= 256.  Replaces the fp64 recurrence of
+ * scripts/gdn_ref_kernel.py:84-87 and the block solve of
+ * example/gdn_native/solve_op/src/gdn_solve_core.h:28-83. */
+qh_status qh_gdn_solve_f32(const float *A_dev, float *T_dev, uint32_t heads, uint32_t C, uint32_t precision,
+                           void *stream);
+
+/* Quantized I/O contract of the reference's GdnSolve op and bare-metal gdnbm_solve
+ * (example/gdn_native/solve_op/src/GdnSolveOp.cpp:185-254; baremetal/inc/gdnbm.idl:7-13):
+ * A_dev uint16 codes [heads][C][C], A = (code - zpA) * sA; T_dev uint16 codes
+ * T_code = clip(rint(T / sT) + zpT, 0, 65535), zeros (= zpT) above the diagonal. */
+qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t heads, uint32_t C, int32_t zpA,
+                           int32_t zpT, float sA, float sT, uint32_t precision, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QHTP_H_ */

@@ -1,0 +1,162 @@
+"""Oracle for the GDN / KDA triangular solve -- TEST INFRASTRUCTURE ONLY.
+
+Functions and the reference lines they follow
+---------------------------------------------
+* ``l2norm``          -- scripts/gdn_ref_kernel.py:31-32 (x / sqrt(sum x^2 + 1e-6)).
+* ``build_A``         -- the strictly-lower A of a chunk, scripts/gdn_ref_kernel.py:71-83:
+                         A_ij = -beta_i (k_i . k_j) exp(g_i - g_j) for i > j, g = cumsum(gc).
+* ``config4_inputs``  -- the synthetic inputs of the C=256 x 32-head solve: k ~ N(0,1) of
+                         dimension 128, beta = sigmoid(N(0,1)), gc = logsigmoid(N(0,1) + 3).
+* ``inverse_fp64``    -- np.linalg.inv(I - A) per head, scripts/gdn_solve_oc_check.py:30.
+* ``forward_subst``   -- the row recurrence T[i,:i] += T[i,:i] @ T[:i,:i], then + I,
+                         scripts/gdn_ref_kernel.py:84-87.
+* ``oc``              -- ||T - Tref||_F / (||Tref||_F + 1e-12), scripts/gdn_solve_oc_check.py:31.
+* ``quantize_u16`` / ``dequantize_u16`` -- the u16 code contract (zp 32768) of
+                         scripts/gdn_solve_oc_check.py:27-29 and GdnSolveOp.cpp:185-254.
+* ``solve_int16_blocks`` -- the reference's int16 block model (BL=16 diagonal forward
+                         substitution on int16 codes at sT = 2/32767 with int32 accumulation,
+                         fp64 block merges): scripts/gdn_solve_int16_model.py:25-56 and
+                         example/gdn_native/solve_op/gdn_solve_ref.c:19-69.
+* ``chunk_uw``        -- U = T (beta * V), W = T (beta * K) [or T (beta * K * e^g)],
+                         scripts/gdn_ref_kernel.py:88-89.
+
+Pinning
+-------
+* ``inverse_fp64`` is LAPACK; it is cross-checked against ``forward_subst`` (independent
+  algorithm), against the identity T (I - A) = I, and against the closed form of the
+  nilpotent Neumann series on small C.
+* ``solve_int16_blocks`` is pinned against the reference's own C model compiled from
+  /root/reference (oracle/_ref/gdn_solve_ref, built by oracle/Makefile) on the same codes.
+* ``build_A`` is pinned by closed-form special cases (beta = 0 -> A = 0; orthogonal keys ->
+  A = 0; a rank-one check on two tokens).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "l2norm",
+    "build_A",
+    "config4_inputs",
+    "inverse_fp64",
+    "forward_subst",
+    "oc",
+    "quantize_u16",
+    "dequantize_u16",
+    "solve_int16_blocks",
+    "chunk_uw",
+    "GATE_BF16",
+    "GATE_FP32",
+    "SA_REF",
+    "ST_REF",
+]
+
+GATE_BF16 = 1.05e-2  # tests/qnn_kernel_e2e/correctness/test_gdn_solve_e2e.sh:18
+GATE_FP32 = 1.0e-4
+SA_REF = 2.770166930875267e-05  # test_gdn_solve_e2e.sh:19
+ST_REF = 6.103701895199438e-05
+
+
+def l2norm(x: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    return x / np.sqrt((x * x).sum(axis=-1, keepdims=True) + eps)
+
+
+def build_A(k: np.ndarray, beta: np.ndarray, gc: np.ndarray) -> np.ndarray:
+    """A [..., C, C] (float64) from keys k [..., C, D], beta [..., C], per-token log decay gc [..., C]."""
+    kn = l2norm(k.astype(np.float64))
+    b = beta.astype(np.float64)
+    g = np.cumsum(gc.astype(np.float64), axis=-1)
+    C = k.shape[-2]
+    diff = g[..., :, None] - g[..., None, :]
+    lower = np.tril(np.ones((C, C), dtype=bool), -1)
+    decay = np.exp(np.where(lower, diff, 0.0)) * lower
+    kk = kn @ np.swapaxes(kn, -1, -2)
+    return -(b[..., :, None] * kk) * decay
+
+
+def config4_inputs(heads: int = 32, C: int = 256, D: int = 128, seed: int = 4):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((heads, C, D))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((heads, C))))
+    z = rng.standard_normal((heads, C)) + 3.0
+    gc = -np.logaddexp(0.0, -z)  # logsigmoid(z)
+    return k, beta, gc
+
+
+def inverse_fp64(A: np.ndarray) -> np.ndarray:
+    A = np.asarray(A, dtype=np.float64)
+    C = A.shape[-1]
+    eye = np.eye(C)
+    flat = A.reshape(-1, C, C)
+    out = np.stack([np.linalg.inv(eye - a) for a in flat])
+    return out.reshape(A.shape)
+
+
+def forward_subst(A: np.ndarray) -> np.ndarray:
+    """(I - A)^-1 by the reference's row recurrence on strictly-lower A (float64)."""
+    A = np.asarray(A, dtype=np.float64)
+    C = A.shape[-1]
+    T = np.tril(A, -1).copy()
+    for i in range(1, C):
+        row = T[..., i, :i].copy()
+        T[..., i, :i] = row + np.einsum("...j,...jk->...k", row, T[..., :i, :i])
+    return T + np.eye(C)
+
+
+def oc(T: np.ndarray, Tref: np.ndarray) -> float:
+    T = np.asarray(T, dtype=np.float64)
+    Tref = np.asarray(Tref, dtype=np.float64)
+    return float(np.linalg.norm(T - Tref) / (np.linalg.norm(Tref) + 1e-12))
+
+
+def quantize_u16(x: np.ndarray, scale: float, zp: int = 32768) -> np.ndarray:
+    return np.clip(np.rint(np.asarray(x, np.float64) / scale) + zp, 0, 65535).astype(np.uint16)
+
+
+def dequantize_u16(codes: np.ndarray, scale: float, zp: int = 32768) -> np.ndarray:
+    return (codes.astype(np.int64) - zp) * scale
+
+
+def solve_int16_blocks(Aq: np.ndarray, sA: float, sT: float, BL: int = 16) -> np.ndarray:
+    """Reference int16 block model on int16 codes Aq [C, C] at scale sA; returns T (float64)."""
+    Aq = np.asarray(Aq, dtype=np.int64)
+    C = Aq.shape[0]
+    nb = C // BL
+    Ti = np.zeros((nb, BL, BL), np.int64)
+    for b in range(nb):
+        d = Aq[b * BL:(b + 1) * BL, b * BL:(b + 1) * BL]
+        Tb = np.zeros((BL, BL), np.int64)
+        for i in range(BL):
+            acc = (d[i, :i][:, None] * Tb[:i, :]).sum(0) if i else np.zeros(BL, np.int64)
+            e = np.zeros(BL)
+            e[i] = 1.0 / sT
+            v = e + acc.astype(np.float64) * sA
+            v = np.clip(v, -32767.0, 32767.0)
+            # llround: half away from zero
+            Tb[i, :] = (np.sign(v) * np.floor(np.abs(v) + 0.5)).astype(np.int64)
+        Ti[b] = Tb
+    blk = {(b, b): Ti[b].astype(np.float64) * sT for b in range(nb)}
+    for i in range(nb):
+        for j in range(i - 1, -1, -1):
+            acc = np.zeros((BL, BL))
+            for k in range(j, i):
+                Aik = Aq[i * BL:(i + 1) * BL, k * BL:(k + 1) * BL].astype(np.float64) * sA
+                acc += Aik @ blk[(k, j)]
+            blk[(i, j)] = blk[(i, i)] @ acc
+    T = np.zeros((C, C))
+    for i in range(nb):
+        for j in range(i + 1):
+            T[i * BL:(i + 1) * BL, j * BL:(j + 1) * BL] = blk[(i, j)]
+    return T
+
+
+def chunk_uw(T: np.ndarray, k: np.ndarray, v: np.ndarray, beta: np.ndarray, gc: np.ndarray, decay_w: bool = False):
+    """U = T (beta * v), W = T (beta * l2norm(k)) [times e^g when decay_w] (float64)."""
+    kn = l2norm(k.astype(np.float64))
+    b = beta.astype(np.float64)[..., None]
+    U = T @ (b * v.astype(np.float64))
+    kb = b * kn
+    if decay_w:
+        kb = kb * np.exp(np.cumsum(gc.astype(np.float64), axis=-1))[..., None]
+    return U, T @ kb

@@ -1,0 +1,148 @@
+// C-ABI entry points of libqhtp: argument validation, error reporting and dispatch to the
+// kernel launchers.  Modelled on the reference's prepared-run ABI
+// (example/handwritten_hmx_matmul/include/handwritten_hmx_matmul.h:11-52), with the
+// difference that an unsupported or invalid shape is always reported, never silently skipped
+// (the reference's QHPI callbacks return success without writing, e.g.
+// HmxU8I8ToU8MatMulOp.cpp:230,246,500,550).
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "qmm_internal.h"
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+namespace qh {
+
+qh_status fail(qh_status st, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+qh_status hip_fail(hipError_t err, const char *what) {
+  return fail(QH_STATUS_RUNTIME_ERROR, "%s: %s", what, hipGetErrorString(err));
+}
+
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" {
+
+const char *qh_status_string(qh_status status) {
+  switch (status) {
+    case QH_STATUS_OK:
+      return "ok";
+    case QH_STATUS_INVALID_ARGUMENT:
+      return "invalid_argument";
+    case QH_STATUS_UNSUPPORTED:
+      return "unsupported";
+    case QH_STATUS_RUNTIME_ERROR:
+      return "runtime_error";
+    case QH_STATUS_SHAPE_UNSUPPORTED:
+      return "shape_unsupported";
+  }
+  return "unknown";
+}
+
+const char *qh_last_error(void) { return g_err; }
+
+uint32_t qh_version(void) { return 0x000100u; }
+
+qh_status qh_qmm_run_path(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
+                          uint32_t path, void *stream) {
+  if (prep == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: prepared handle is NULL");
+  if (m == 0) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_qmm_run: M must be >= 1");
+  if (m > (1u << 24)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_qmm_run: M=%u too large", m);
+  if (act_dev == nullptr || out_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: NULL buffer");
+  const size_t ea = prep->shape.act_bits == 16 ? 2 : 1;
+  if (reinterpret_cast<uintptr_t>(act_dev) % 16 || (static_cast<size_t>(prep->shape.K) * ea) % 16)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: activation rows must be 16-byte aligned");
+  if (path > 2) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: unknown path %u", path);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool gemv = path == 2 || (path == 0 && m <= 16);
+  if (gemv) return launch_qmm_gemv(prep, static_cast<int>(m), act_dev, out_dev, s);
+  return launch_qmm_gemm(prep, static_cast<int>(m), act_dev, out_dev, s);
+}
+
+qh_status qh_qmm_run(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev, void *stream) {
+  return qh_qmm_run_path(prep, m, act_dev, out_dev, 0, stream);
+}
+
+qh_status qh_qmm_accumulate(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, int64_t *acc_dev,
+                            void *stream) {
+  if (prep == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_accumulate: prepared handle is NULL");
+  if (m == 0 || m > (1u << 24)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_qmm_accumulate: bad M=%u", m);
+  if (act_dev == nullptr || acc_dev == nullptr)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_accumulate: NULL buffer");
+  if (reinterpret_cast<uintptr_t>(act_dev) % 16)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_accumulate: activation must be 16-byte aligned");
+  return launch_qmm_accumulate(prep, static_cast<int>(m), act_dev, acc_dev, static_cast<hipStream_t>(stream));
+}
+
+qh_status qh_qmm_query(const qh_qmm_prepared *prep, qh_qmm_info *info) {
+  if (prep == nullptr || info == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_query: NULL argument");
+  const QmmShape &sh = prep->shape;
+  info->k = static_cast<uint32_t>(sh.K);
+  info->n = static_cast<uint32_t>(sh.N);
+  info->act_bits = static_cast<uint32_t>(sh.act_bits);
+  info->out_bits = static_cast<uint32_t>(sh.out_bits);
+  info->weight_format = static_cast<uint32_t>(sh.wfmt);
+  info->lpbq_block = static_cast<uint32_t>(sh.lpbq_block);
+  info->device_bytes = prep->device_bytes;
+  info->gemm_weight_bytes = prep->gemm_weight_bytes;
+  info->gemv_weight_bytes = prep->gemv_weight_bytes;
+  return QH_STATUS_OK;
+}
+
+qh_status qh_qmm_release(qh_qmm_prepared *prep) {
+  if (prep == nullptr) return QH_STATUS_OK;
+  int cur = 0;
+  (void)hipGetDevice(&cur);
+  (void)hipSetDevice(prep->device_id);
+  hipError_t err = hipDeviceSynchronize();
+  QmmDevice &D = prep->dev;
+  void *ptrs[] = {D.tiles, D.lpbq_tiles, D.gemv_tiles, D.gemv_lpbq, D.alpha, D.beta, D.corr,
+                  D.margin, D.absb, D.bias_deq, D.s32, D.mant, D.colsum, D.gemv_margin_r1};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  (void)hipSetDevice(cur);
+  delete prep;
+  if (err != hipSuccess) return hip_fail(err, "qh_qmm_release");
+  return QH_STATUS_OK;
+}
+
+qh_status qh_gdn_solve_f32(const float *A_dev, float *T_dev, uint32_t heads, uint32_t C, uint32_t precision,
+                           void *stream) {
+  if (A_dev == nullptr || T_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_f32: NULL buffer");
+  if (heads == 0 || heads > (1u << 24)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_f32: bad heads=%u", heads);
+  if (C < 16 || C > 256 || C % 16) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_f32: C=%u (need 16..256, C%%16==0)", C);
+  if (precision > QH_GDN_BF16) return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_solve_f32: unknown precision %u", precision);
+  if (reinterpret_cast<uintptr_t>(A_dev) % 16 || reinterpret_cast<uintptr_t>(T_dev) % 16)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_f32: buffers must be 16-byte aligned");
+  return launch_gdn_solve_f32(A_dev, T_dev, static_cast<int>(heads), static_cast<int>(C), static_cast<int>(precision),
+                              static_cast<hipStream_t>(stream));
+}
+
+qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t heads, uint32_t C, int32_t zpA, int32_t zpT,
+                           float sA, float sT, uint32_t precision, void *stream) {
+  if (A_dev == nullptr || T_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: NULL buffer");
+  if (heads == 0 || heads > (1u << 24)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_u16: bad heads=%u", heads);
+  if (C < 16 || C > 256 || C % 16) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_u16: C=%u (need 16..256, C%%16==0)", C);
+  if (precision > QH_GDN_BF16) return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_solve_u16: unknown precision %u", precision);
+  if (zpA < 0 || zpA > 65535 || zpT < 0 || zpT > 65535)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: zero points must be in [0, 65535]");
+  if (!(sA > 0.0f) || !(sT > 0.0f)) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: scales must be > 0");
+  if (reinterpret_cast<uintptr_t>(A_dev) % 16 || reinterpret_cast<uintptr_t>(T_dev) % 16)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: buffers must be 16-byte aligned");
+  return launch_gdn_solve_u16(A_dev, T_dev, static_cast<int>(heads), static_cast<int>(C), zpA, zpT, sA, sT,
+                              static_cast<int>(precision), static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

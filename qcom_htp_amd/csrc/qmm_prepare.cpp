@@ -1,0 +1,339 @@
+// Host-side prepare step of the quantized matmul: validates the descriptor, lays the weight
+// codes out as MFMA/streaming tiles, and derives the per-channel epilogue constants that make
+// the integer-accumulator result bit-exact to the reference's float-derived requantisation.
+//
+// Reference correspondence: the QHPI precompute of the op packages
+// (example/qnn_hmx_matmul_u8i8/src/HmxU8I8ToU8MatMulOp.cpp:196-287) and the const-folded LPBQ
+// expansion (example/qnn_hmx_matmul_common/HmxW4LpbqExpandToI8Op.cpp:107-164) both run once
+// at graph prepare; this file is that step for the GPU.
+//
+// Exactness argument (why the epilogue can round like the float64 oracle):
+//   The oracle dequantises weights as w_deq = fl32(w_int * s32).  Write s32 = M * 2^E with a
+//   24-bit integer mantissa M.  Every w_deq is then an integer multiple W' of 2^E with
+//   W' = w_int * M + r, where r is the float32 rounding residue (|r| <= 64 for |w_int| <= 127).
+//   The exact dot product is  sum_k (a_k - zp) * w_deq_k = 2^E * (M * acc + sum_k (a_k - zp) r_k)
+//   with acc the int32 MFMA accumulator.
+//   * 16-bit activations: the kernels accumulate sum (a - zp) * r as well (the residue plane is
+//     a second weight operand), so the exact dot product is known in int64.
+//   * 8-bit activations: the residue term is bounded by amax * sum_k |r_k| per channel
+//     (amax = max |a - zp|); outputs whose rounding could flip within that bound are recomputed
+//     exactly by the kernel's fixup pass.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <vector>
+
+#include "qmm_internal.h"
+
+namespace qh {
+namespace {
+
+constexpr double kSafety = 1.0 + 1.0 / 1048576.0;  // 1 + 2^-20 on every bound
+
+inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// s32 = M * 2^E with M a 24-bit integer (for normal floats M in [2^23, 2^24)).
+inline void split_float(float s, int64_t *M, int *E) {
+  int e = 0;
+  double fr = std::frexp(static_cast<double>(s), &e);  // s = fr * 2^e, fr in [0.5, 1)
+  *M = static_cast<int64_t>(std::ldexp(fr, 24));
+  *E = e - 24;
+}
+
+struct DevAlloc {
+  std::vector<void *> ptrs;
+  uint64_t bytes = 0;
+  template <class T>
+  qh_status upload(T **dst, const std::vector<T> &src) {
+    *dst = nullptr;
+    if (src.empty()) return QH_STATUS_OK;
+    size_t nbytes = src.size() * sizeof(T);
+    void *p = nullptr;
+    hipError_t err = hipMalloc(&p, nbytes);
+    if (err != hipSuccess) return hip_fail(err, "hipMalloc(prepared state)");
+    ptrs.push_back(p);
+    bytes += nbytes;
+    err = hipMemcpy(p, src.data(), nbytes, hipMemcpyHostToDevice);
+    if (err != hipSuccess) return hip_fail(err, "hipMemcpy(prepared state)");
+    *dst = static_cast<T *>(p);
+    return QH_STATUS_OK;
+  }
+  void release() {
+    for (void *p : ptrs) (void)hipFree(p);
+    ptrs.clear();
+  }
+};
+
+// Writes value v (int8 range) of operand column c, depth k into the tile image.
+struct TileWriter {
+  std::vector<uint8_t> &buf;
+  int fmt;
+  int KT;  // number of 128-deep k tiles
+  void put(int c, int k, int v) {
+    size_t tile = static_cast<size_t>(c / kBN) * KT + k / kBK;
+    int cc = c % kBN, kk = k % kBK;
+    if (fmt == kTileI8) {
+      buf[tile * (kBN * kBK) + static_cast<size_t>(cc) * kBK + kk] = static_cast<uint8_t>(static_cast<int8_t>(v));
+    } else {
+      size_t off = tile * (kBN * kBK / 2) + static_cast<size_t>(cc) * (kBK / 2) + (kk / 16) * 8 + (kk % 16) % 8;
+      uint8_t nib = static_cast<uint8_t>((v + 8) & 15);
+      if ((kk % 16) < 8)
+        buf[off] = static_cast<uint8_t>((buf[off] & 0xF0) | nib);
+      else
+        buf[off] = static_cast<uint8_t>((buf[off] & 0x0F) | (nib << 4));
+    }
+  }
+  static size_t bytes_for(int fmt, int ncols, int Kp) {
+    return static_cast<size_t>(ncols) * Kp / (fmt == kTileI8 ? 1 : 2);
+  }
+  static uint8_t zero_byte(int fmt) { return fmt == kTileI8 ? 0x00 : 0x88; }
+};
+
+}  // namespace
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out) {
+  if (out == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_prepare: out is NULL");
+  *out = nullptr;
+  if (d == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_prepare: desc is NULL");
+  if (d->act_bits != 8 && d->act_bits != 16)
+    return fail(QH_STATUS_UNSUPPORTED, "act_bits must be 8 or 16 (got %u)", d->act_bits);
+  if (d->out_bits != 8 && d->out_bits != 16)
+    return fail(QH_STATUS_UNSUPPORTED, "out_bits must be 8 or 16 (got %u)", d->out_bits);
+  if (d->weight_format > QH_WEIGHT_I4_LPBQ)
+    return fail(QH_STATUS_UNSUPPORTED, "unknown weight_format %u", d->weight_format);
+  if (d->k == 0 || d->n == 0 || d->k % 32 || d->n % 32)
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "K and N must be positive multiples of 32 (K=%u N=%u)", d->k, d->n);
+  if (d->k > 65536 || d->n > (1u << 20))
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "K <= 65536 and N <= 2^20 required (K=%u N=%u)", d->k, d->n);
+  const bool lpbq = d->weight_format == QH_WEIGHT_I4_LPBQ;
+  if (lpbq && d->lpbq_block != 32 && d->lpbq_block != 64)
+    return fail(QH_STATUS_UNSUPPORTED, "lpbq_block must be 32 or 64 (got %u)", d->lpbq_block);
+  if (lpbq && d->k % d->lpbq_block)
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "K=%u must be a multiple of lpbq_block=%u", d->k, d->lpbq_block);
+  if (d->weight_nk == nullptr || d->weight_scale == nullptr || (lpbq && d->lpbq_block_scale == nullptr))
+    return fail(QH_STATUS_INVALID_ARGUMENT, "weight_nk / weight_scale / lpbq_block_scale is NULL");
+  const int act_qmax = (1 << d->act_bits) - 1, out_qmax = (1 << d->out_bits) - 1;
+  if (d->act_zp < 0 || d->act_zp > act_qmax || d->out_zp < 0 || d->out_zp > out_qmax)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "zero point out of range (act_zp=%d out_zp=%d)", d->act_zp, d->out_zp);
+  if (!(d->act_scale > 0.0) || !(d->out_scale > 0.0) || !std::isfinite(d->act_scale) || !std::isfinite(d->out_scale))
+    return fail(QH_STATUS_INVALID_ARGUMENT, "act_scale and out_scale must be finite and > 0");
+
+  const int N = static_cast<int>(d->n), K = static_cast<int>(d->k);
+  const int wq_max = d->weight_format == QH_WEIGHT_I8 ? 127 : 7;
+  const int bs = lpbq ? static_cast<int>(d->lpbq_block) : 0;
+  const int nblk = lpbq ? K / bs : 0;
+
+  // ---- integer weights, scale mantissas, rounding residues --------------------------------
+  std::vector<int8_t> wint(static_cast<size_t>(N) * K);
+  std::vector<int8_t> resid(static_cast<size_t>(N) * K);
+  std::vector<int64_t> mant(N), colsum_q(N), colsum_r(N);
+  std::vector<int> expo(N), rmax(N);
+  std::vector<double> r1(N), wpmax(N);
+  for (int n = 0; n < N; ++n) {
+    const float s = d->weight_scale[n];
+    if (!(s > 0.0f) || !std::isfinite(s) || s < std::numeric_limits<float>::min())
+      return fail(QH_STATUS_INVALID_ARGUMENT, "weight_scale[%d] must be a positive normal float", n);
+    int64_t M;
+    int E;
+    split_float(s, &M, &E);
+    mant[n] = M;
+    expo[n] = E;
+    int64_t cq = 0, cr = 0;
+    double ra = 0, wm = 0;
+    int rm = 0;
+    for (int k = 0; k < K; ++k) {
+      int q = d->weight_nk[static_cast<size_t>(n) * K + k];
+      if (q < -wq_max || q > wq_max)
+        return fail(QH_STATUS_INVALID_ARGUMENT, "weight code %d at (n=%d,k=%d) outside [-%d,%d]", q, n, k, wq_max, wq_max);
+      int w = q;
+      if (lpbq) {
+        int f = d->lpbq_block_scale[static_cast<size_t>(n) * nblk + k / bs];
+        if (f < 1 || f > 16)
+          return fail(QH_STATUS_INVALID_ARGUMENT, "LPBQ block scale %d at (n=%d,block=%d) outside [1,16]", f, n, k / bs);
+        w = q * f;  // |w| <= 112: exact, no saturation
+      }
+      // The oracle's float32 product, then its exact integer multiple of 2^E.
+      const float wd = static_cast<float>(w) * s;
+      const double wp = std::ldexp(static_cast<double>(wd), -E);
+      const int64_t Wp = static_cast<int64_t>(wp);
+      if (static_cast<double>(Wp) != wp) return fail(QH_STATUS_RUNTIME_ERROR, "internal: non-integer residue at n=%d", n);
+      const int64_t r = Wp - static_cast<int64_t>(w) * M;
+      if (r < -127 || r > 127) return fail(QH_STATUS_RUNTIME_ERROR, "internal: residue %lld out of int8", (long long)r);
+      wint[static_cast<size_t>(n) * K + k] = static_cast<int8_t>(w);
+      resid[static_cast<size_t>(n) * K + k] = static_cast<int8_t>(r);
+      cq += w;
+      cr += r;
+      ra += std::fabs(static_cast<double>(r));
+      rm = std::max(rm, static_cast<int>(std::llabs(r)));
+      wm = std::max(wm, std::fabs(wp));
+    }
+    colsum_q[n] = cq;
+    colsum_r[n] = cr;
+    r1[n] = ra;
+    rmax[n] = rm;
+    wpmax[n] = wm;
+  }
+
+  // ---- shape / format decisions ------------------------------------------------------------
+  QmmShape sh{};
+  sh.N = N;
+  sh.K = K;
+  sh.Kp = round_up(K, kBK);
+  sh.act_bits = static_cast<int>(d->act_bits);
+  sh.out_bits = static_cast<int>(d->out_bits);
+  sh.wfmt = static_cast<int>(d->weight_format);
+  sh.lpbq_block = bs;
+  sh.act_zp = d->act_zp;
+  sh.out_zp = d->out_zp;
+  sh.act_scale = d->act_scale;
+  sh.out_scale = d->out_scale;
+  const bool a16 = d->act_bits == 16;
+  bool resid_fits_nibble = true;
+  for (size_t i = 0; i < resid.size() && resid_fits_nibble; ++i) resid_fits_nibble = resid[i] >= -8 && resid[i] <= 7;
+  if (!a16) {
+    sh.tile_fmt = d->weight_format == QH_WEIGHT_I8 ? kTileI8 : kTileI4;
+    sh.ncols_op = round_up(N, kBN);
+    sh.Np = sh.ncols_op;
+  } else {
+    // codes and residues share one operand; nibbles only when both fit.
+    sh.tile_fmt = (d->weight_format == QH_WEIGHT_I4 && resid_fits_nibble) ? kTileI4 : kTileI8;
+    sh.ncols_op = round_up(2 * N, kBN);
+    sh.Np = sh.ncols_op / 2;
+  }
+  sh.gemv_fmt = d->weight_format == QH_WEIGHT_I8 ? kTileI8 : kTileI4;
+  const int KT = sh.Kp / kBK;
+
+  // ---- GEMM operand tiles ------------------------------------------------------------------
+  std::vector<uint8_t> tiles(TileWriter::bytes_for(sh.tile_fmt, sh.ncols_op, sh.Kp), TileWriter::zero_byte(sh.tile_fmt));
+  TileWriter tw{tiles, sh.tile_fmt, KT};
+  std::vector<uint8_t> lpbq_tiles;
+  const bool gemm_lpbq_regs = lpbq && !a16;  // LPBQ expanded in registers by the A8 GEMM
+  if (!a16) {
+    for (int n = 0; n < N; ++n)
+      for (int k = 0; k < K; ++k) {
+        int v = gemm_lpbq_regs ? d->weight_nk[static_cast<size_t>(n) * K + k] : wint[static_cast<size_t>(n) * K + k];
+        tw.put(n, k, v);
+      }
+    if (gemm_lpbq_regs) {
+      const int nb = sh.Kp / bs;
+      lpbq_tiles.assign(static_cast<size_t>(sh.ncols_op) * nb, 1);
+      for (int n = 0; n < N; ++n)
+        for (int b = 0; b < nblk; ++b) lpbq_tiles[static_cast<size_t>(n) * nb + b] = d->lpbq_block_scale[static_cast<size_t>(n) * nblk + b];
+    }
+  } else {
+    for (int n = 0; n < N; ++n) {
+      const int cq = (n / 32) * 64 + (n % 32), cr = cq + 32;
+      for (int k = 0; k < K; ++k) {
+        tw.put(cq, k, wint[static_cast<size_t>(n) * K + k]);
+        tw.put(cr, k, resid[static_cast<size_t>(n) * K + k]);
+      }
+    }
+  }
+
+  // ---- GEMV stream (weights read once per call) --------------------------------------------
+  // [N/16 column groups][K/32 k-groups][16 columns][16 B int4 | 32 B int8]; int4 byte j of a
+  // (column, k-group) holds k = j in its low nibble and k = j + 16 in its high nibble.
+  std::vector<uint8_t> gemv_tiles, gemv_lpbq;
+  {
+    const int KG = K / 32;
+    const int per = sh.gemv_fmt == kTileI8 ? 32 : 16;
+    gemv_tiles.assign(static_cast<size_t>(N) * KG * per, 0);
+    for (int n = 0; n < N; ++n)
+      for (int kg = 0; kg < KG; ++kg) {
+        uint8_t *dst = &gemv_tiles[((static_cast<size_t>(n / 16) * KG + kg) * 16 + (n % 16)) * per];
+        const int8_t *src = (lpbq ? d->weight_nk : wint.data()) + static_cast<size_t>(n) * K + kg * 32;
+        if (sh.gemv_fmt == kTileI8) {
+          for (int j = 0; j < 32; ++j) dst[j] = static_cast<uint8_t>(src[j]);
+        } else {
+          for (int j = 0; j < 16; ++j)
+            dst[j] = static_cast<uint8_t>(((src[j] + 8) & 15) | (((src[j + 16] + 8) & 15) << 4));
+        }
+      }
+    if (lpbq) {
+      gemv_lpbq.assign(static_cast<size_t>(N) * nblk, 1);
+      for (int n = 0; n < N; ++n)
+        for (int b = 0; b < nblk; ++b)
+          gemv_lpbq[(static_cast<size_t>(n / 16) * nblk + b) * 16 + (n % 16)] =
+              d->lpbq_block_scale[static_cast<size_t>(n) * nblk + b];
+    }
+  }
+
+  // ---- epilogue constants ------------------------------------------------------------------
+  const double sA = d->act_scale, sO = d->out_scale, inv_sO = 1.0 / sO;
+  const double amax = static_cast<double>(std::max(d->act_zp, act_qmax - d->act_zp));
+  const int Np = sh.Np;
+  std::vector<double> alpha(Np, 0.0), beta(Np, 0.0), margin(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0), mr1(Np, 0.0);
+  std::vector<int64_t> corr(Np, 0), mantv(Np, 0), csum(Np, 0);
+  std::vector<float> s32v(Np, 1.0f);
+  const double a_base = a16 ? 32768.0 : 128.0;  // the kernels shift activations by this
+  for (int n = 0; n < N; ++n) {
+    const float s = d->weight_scale[n];
+    const double c1 = sA * static_cast<double>(s);  // fl64(sA * s32): the oracle's bias scale
+    const double bq = d->bias_q ? static_cast<double>(d->bias_q[n]) : 0.0;
+    bdeq[n] = bq * c1;
+    const double two_e = std::ldexp(1.0, expo[n]);
+    // Float noise of the oracle's own float64 dot product (|sum of terms| bound).
+    const double noise = (K + 8.0) * std::ldexp(1.0, -52) * K * amax * wpmax[n];
+    if (!a16) {
+      alpha[n] = c1 / sO;
+      corr[n] = static_cast<int64_t>(a_base - d->act_zp) * colsum_q[n];
+      margin[n] = inv_sO * sA * two_e * (amax * r1[n] + noise) * kSafety;
+    } else {
+      alpha[n] = sA * two_e / sO;
+      const int64_t sum_wp = mant[n] * colsum_q[n] + colsum_r[n];
+      corr[n] = static_cast<int64_t>(128 + 32768 - d->act_zp) * sum_wp;
+      margin[n] = inv_sO * sA * two_e * noise * kSafety;
+      mr1[n] = inv_sO * sA * two_e * rmax[n] * kSafety;  // GEMV: residue term bound per unit R1
+    }
+    beta[n] = bdeq[n] / sO + d->out_zp;
+    absb[n] = 2.0 * std::fabs(beta[n]) + 2.0 * d->out_zp + 1.0;
+    mantv[n] = mant[n];
+    csum[n] = colsum_q[n];
+    s32v[n] = s;
+  }
+
+  // ---- upload -------------------------------------------------------------------------------
+  auto *p = new qh_qmm_prepared();
+  p->shape = sh;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  p->device_id = dev;
+  DevAlloc al;
+  qh_status st = QH_STATUS_OK;
+  QmmDevice &D = p->dev;
+  std::memset(&D, 0, sizeof(D));
+  if (st == QH_STATUS_OK) st = al.upload(&D.tiles, tiles);
+  if (st == QH_STATUS_OK) st = al.upload(&D.lpbq_tiles, lpbq_tiles);
+  if (st == QH_STATUS_OK) st = al.upload(&D.gemv_tiles, gemv_tiles);
+  if (st == QH_STATUS_OK) st = al.upload(&D.gemv_lpbq, gemv_lpbq);
+  if (st == QH_STATUS_OK) st = al.upload(&D.alpha, alpha);
+  if (st == QH_STATUS_OK) st = al.upload(&D.beta, beta);
+  if (st == QH_STATUS_OK) st = al.upload(&D.corr, corr);
+  if (st == QH_STATUS_OK) st = al.upload(&D.margin, margin);
+  if (st == QH_STATUS_OK) st = al.upload(&D.absb, absb);
+  if (st == QH_STATUS_OK) st = al.upload(&D.bias_deq, bdeq);
+  if (st == QH_STATUS_OK) st = al.upload(&D.s32, s32v);
+  if (st == QH_STATUS_OK) st = al.upload(&D.mant, mantv);
+  if (st == QH_STATUS_OK) st = al.upload(&D.colsum, csum);
+  if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
+  if (st != QH_STATUS_OK) {
+    al.release();
+    delete p;
+    return st;
+  }
+  p->device_bytes = al.bytes;
+  p->gemm_weight_bytes = tiles.size() + lpbq_tiles.size();
+  // Bytes one GEMV call must stream: packed codes (+ block scales) of the logical N x K.
+  {
+    const uint64_t codes = static_cast<uint64_t>(N) * K / (sh.gemv_fmt == kTileI8 ? 1 : 2);
+    const uint64_t scales = lpbq ? static_cast<uint64_t>(N) * (K / bs) : 0;
+    p->gemv_weight_bytes = codes + scales;
+  }
+  *out = p;
+  return QH_STATUS_OK;
+}

@@ -1,0 +1,168 @@
+"""QNN-semantics quantized matmul on MI355X.
+
+``QuantMatmul`` is the prepared op: construct it once from the weight codes and quantisation
+parameters (the reference's graph-prepare / QHPI precompute), then call it on device
+activations (the reference's hot op callback).  All arithmetic runs in libqhtp's HIP kernels;
+this module only marshals arguments.
+
+Family naming follows the reference (scripts/generate_qnn_matmul_python_cases.py:74-125):
+u8i8, w4a8_per_channel, w4a8_lpbq, w8a16, w4a16_per_channel, w4a16_lpbq.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import _lib
+from .cases import FAMILIES, Family, QmmCase
+
+PATH_AUTO, PATH_GEMM, PATH_GEMV = 0, 1, 2
+
+__all__ = ["QuantMatmul", "PATH_AUTO", "PATH_GEMM", "PATH_GEMV", "weight_format_of"]
+
+
+def weight_format_of(family: Family) -> int:
+    if family.weight_schema == "lpbq_blockwise_expansion":
+        return _lib.QH_WEIGHT_I4_LPBQ
+    if family.weight_schema != "per_output_channel":
+        raise ValueError(f"{family.name}: weight schema {family.weight_schema!r} is not supported")
+    return _lib.QH_WEIGHT_I8 if family.weight_bits == 8 else _lib.QH_WEIGHT_I4
+
+
+def _stream_ptr(stream: Optional[torch.cuda.Stream]) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+class QuantMatmul:
+    """out[M,N] = clip(rint(((act - act_zp) sA) @ fl32(w_int s32).T + bias_deq) / sO + out_zp)).
+
+    Parameters mirror the reference case (``case.json`` qparams): ``weight_q_nk`` int codes
+    [N,K]; ``weight_scale`` float32 [N]; ``bias_q`` int32 [N]; ``lpbq_block_scale`` uint8
+    [N, K/block] for LPBQ; activation/output bit widths, scales and zero points.
+    """
+
+    def __init__(
+        self,
+        weight_q_nk: np.ndarray,
+        weight_scale: np.ndarray,
+        bias_q: Optional[np.ndarray],
+        *,
+        act_bits: int,
+        out_bits: int,
+        act_scale: float,
+        out_scale: float,
+        act_zp: int,
+        out_zp: int,
+        weight_format: int,
+        lpbq_block_scale: Optional[np.ndarray] = None,
+        lpbq_block: int = 0,
+        device: Optional[torch.device] = None,
+    ):
+        w = np.ascontiguousarray(weight_q_nk, dtype=np.int8)
+        n, k = w.shape
+        s32 = np.ascontiguousarray(weight_scale, dtype=np.float32).reshape(n)
+        b = None if bias_q is None else np.ascontiguousarray(bias_q, dtype=np.int32).reshape(n)
+        blk = None
+        if weight_format == _lib.QH_WEIGHT_I4_LPBQ:
+            if lpbq_block_scale is None or lpbq_block not in (32, 64):
+                raise ValueError("LPBQ needs lpbq_block_scale and lpbq_block in {32, 64}")
+            blk = np.ascontiguousarray(lpbq_block_scale, dtype=np.uint8).reshape(n, k // lpbq_block)
+        self.n, self.k = n, k
+        self.act_bits, self.out_bits = act_bits, out_bits
+        self.act_dtype = torch.uint16 if act_bits == 16 else torch.uint8
+        self.out_dtype = torch.uint16 if out_bits == 16 else torch.uint8
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        desc = _lib.QmmDesc(
+            k=k,
+            n=n,
+            act_bits=act_bits,
+            out_bits=out_bits,
+            weight_format=weight_format,
+            lpbq_block=lpbq_block if blk is not None else 0,
+            act_zp=int(act_zp),
+            out_zp=int(out_zp),
+            act_scale=float(act_scale),
+            out_scale=float(out_scale),
+            weight_nk=w.ctypes.data,
+            lpbq_block_scale=blk.ctypes.data if blk is not None else None,
+            weight_scale=s32.ctypes.data,
+            bias_q=b.ctypes.data if b is not None else None,
+        )
+        handle = C.c_void_p()
+        L = _lib.lib()
+        with torch.cuda.device(self.device):
+            _lib.check(L.qh_qmm_prepare(C.byref(desc), C.byref(handle)), "qh_qmm_prepare")
+        self._h = handle
+        info = _lib.QmmInfo()
+        _lib.check(L.qh_qmm_query(self._h, C.byref(info)), "qh_qmm_query")
+        self.info = {f: getattr(info, f) for f, _ in _lib.QmmInfo._fields_}
+
+    # ------------------------------------------------------------------ construction helpers
+    @classmethod
+    def from_case(cls, case: QmmCase, device=None) -> "QuantMatmul":
+        fam = case.family
+        fmt = weight_format_of(fam)
+        return cls(
+            case.weight_q_nk,
+            case.weight_scale,
+            case.bias_q,
+            act_bits=fam.act_bits,
+            out_bits=fam.out_bits,
+            act_scale=case.act_scale,
+            out_scale=case.out_scale,
+            act_zp=fam.act_zp,
+            out_zp=fam.out_zp,
+            weight_format=fmt,
+            lpbq_block_scale=case.lpbq_block_int_scale,
+            lpbq_block=fam.lpbq_block_size if fmt == _lib.QH_WEIGHT_I4_LPBQ else 0,
+            device=device,
+        )
+
+    # ------------------------------------------------------------------ execution
+    def _check_act(self, act: torch.Tensor) -> int:
+        if not isinstance(act, torch.Tensor) or act.device.type != "cuda":
+            raise TypeError("activation must be a CUDA (HIP) tensor")
+        if act.dtype != self.act_dtype:
+            raise TypeError(f"activation dtype must be {self.act_dtype}, got {act.dtype}")
+        if act.dim() != 2 or act.shape[1] != self.k or not act.is_contiguous():
+            raise ValueError(f"activation must be contiguous [M, {self.k}], got {tuple(act.shape)}")
+        return act.shape[0]
+
+    def __call__(self, act: torch.Tensor, out: Optional[torch.Tensor] = None, path: int = PATH_AUTO,
+                 stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        m = self._check_act(act)
+        if out is None:
+            out = torch.empty((m, self.n), dtype=self.out_dtype, device=act.device)
+        elif out.shape != (m, self.n) or out.dtype != self.out_dtype or not out.is_contiguous():
+            raise ValueError("bad output tensor")
+        st = _lib.lib().qh_qmm_run_path(self._h, m, act.data_ptr(), out.data_ptr(), path, _stream_ptr(stream))
+        _lib.check(st, "qh_qmm_run")
+        return out
+
+    def accumulate(self, act: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """Exact int64 accumulators sum_k (act - act_zp) * w_int, [M, N]."""
+        m = self._check_act(act)
+        acc = torch.empty((m, self.n), dtype=torch.int64, device=act.device)
+        st = _lib.lib().qh_qmm_accumulate(self._h, m, act.data_ptr(), acc.data_ptr(), _stream_ptr(stream))
+        _lib.check(st, "qh_qmm_accumulate")
+        return acc
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            _lib.lib().qh_qmm_release(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def family(name: str) -> Family:
+    return FAMILIES[name]

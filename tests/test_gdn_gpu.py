@@ -1,0 +1,99 @@
+"""GPU parity of the GDN triangular solve vs the fp64 inverse.
+
+Tolerances (relative Frobenius error, scripts/gdn_solve_oc_check.py:31):
+  fp32 path  <= 1e-4
+  bf16 path  <= 1.05e-2 (tests/qnn_kernel_e2e/correctness/test_gdn_solve_e2e.sh:18)
+"""
+
+import numpy as np
+import pytest
+
+from oracle import gdn as og
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1.0e-4
+BF16_TOL = 1.05e-2
+
+
+def solve(A, gpu, precision):
+    import torch
+
+    from qcom_htp_amd.gdn import gdn_solve
+
+    t = torch.from_numpy(np.ascontiguousarray(A, dtype=np.float32)).to(gpu)
+    T = gdn_solve(t, precision=precision)
+    torch.cuda.synchronize()
+    return T.cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("C", [16, 32, 48, 64, 128, 256])
+@pytest.mark.parametrize("precision", [0, 1], ids=["fp32", "bf16"])
+def test_gdn_solve_config4_inputs(gpu, C, precision):
+    heads = 8 if C == 256 else 6
+    k, beta, gc = og.config4_inputs(heads=heads, C=C, seed=C)
+    A = og.build_A(k, beta, gc).astype(np.float32)
+    print(f"[gdn] C={C} heads={heads} precision={precision}", flush=True)
+    T = solve(A, gpu, precision)
+    Tref = og.inverse_fp64(A.astype(np.float64))
+    err = og.oc(T, Tref)
+    tol = FP32_TOL if precision == 0 else BF16_TOL
+    assert err <= tol, f"oc={err:.3e} > {tol:.1e}"
+    # exact structure: zeros above the diagonal, unit diagonal
+    iu = np.triu_indices(C, 1)
+    assert np.all(T[:, iu[0], iu[1]] == 0.0)
+    if precision == 0:
+        np.testing.assert_allclose(np.diagonal(T, axis1=1, axis2=2), 1.0, atol=1e-6)
+
+
+def test_gdn_solve_full_config4(gpu):
+    k, beta, gc = og.config4_inputs(heads=32, C=256, seed=4)
+    A = og.build_A(k, beta, gc).astype(np.float32)
+    Tref = og.inverse_fp64(A.astype(np.float64))
+    for precision, tol in ((0, FP32_TOL), (1, BF16_TOL)):
+        print(f"[gdn] config4 32x256 precision={precision}", flush=True)
+        err = og.oc(solve(A, gpu, precision), Tref)
+        assert err <= tol, f"precision {precision}: oc={err:.3e}"
+
+
+def test_gdn_zero_and_identity_cases(gpu):
+    A = np.zeros((2, 64, 64), np.float32)
+    T = solve(A, gpu, 0)
+    np.testing.assert_array_equal(T, np.broadcast_to(np.eye(64), T.shape))
+    # a single sub-diagonal: T is the closed-form nilpotent series sum_k A^k
+    A = np.zeros((1, 32, 32), np.float32)
+    idx = np.arange(31)
+    A[0, idx + 1, idx] = 0.5
+    T = solve(A, gpu, 0)[0]
+    want = np.tril(0.5 ** (np.arange(32)[:, None] - np.arange(32)[None, :]).astype(np.float64))
+    np.testing.assert_allclose(T, want, rtol=1e-6, atol=1e-7)
+
+
+def test_gdn_upper_triangle_is_ignored(gpu):
+    k, beta, gc = og.config4_inputs(heads=2, C=64, seed=9)
+    A = og.build_A(k, beta, gc).astype(np.float32)
+    A_dirty = A + np.triu(np.full((64, 64), 7.0, np.float32))
+    np.testing.assert_array_equal(solve(A, gpu, 0), solve(A_dirty, gpu, 0))
+
+
+@pytest.mark.parametrize("precision", [0, 1], ids=["fp32", "bf16"])
+def test_gdn_u16_code_contract(gpu, precision):
+    import torch
+
+    from qcom_htp_amd.gdn import GdnSolve
+
+    heads, C = 8, 256
+    k, beta, gc = og.config4_inputs(heads=heads, C=C, seed=21)
+    A = og.build_A(k, beta, gc)
+    sA, sT = og.SA_REF, og.ST_REF
+    Aq = og.quantize_u16(A, sA)
+    Adeq = og.dequantize_u16(Aq, sA)
+    print(f"[gdn] u16 contract precision={precision}", flush=True)
+    Tq = GdnSolve(torch.from_numpy(Aq.view(np.uint16)).to(gpu), 32768, sA, 32768, sT, precision=precision)
+    torch.cuda.synchronize()
+    T = og.dequantize_u16(Tq.cpu().numpy(), sT)
+    err = og.oc(T, og.inverse_fp64(Adeq))
+    # u16 output quantisation at sT adds ~sT/sqrt(12) per element on top of the solve error
+    tol = 5e-4 if precision == 0 else BF16_TOL
+    assert err <= tol, f"oc={err:.3e}"
+    assert np.all(Tq.cpu().numpy()[:, np.triu_indices(C, 1)[0], np.triu_indices(C, 1)[1]] == 32768)

@@ -1,0 +1,95 @@
+"""CPU tests pinning the GDN oracle: independent algorithms agree, closed forms hold, and the
+int16 block model matches the reference's own C model compiled from its sources."""
+
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import gdn as og
+
+REF_DIR = Path(__file__).resolve().parents[1] / "oracle" / "_ref"
+
+
+def test_inverse_agrees_with_forward_substitution():
+    k, beta, gc = og.config4_inputs(heads=4, C=64, seed=1)
+    A = og.build_A(k, beta, gc)
+    T1 = og.inverse_fp64(A)
+    T2 = og.forward_subst(A)
+    assert og.oc(T2, T1) < 1e-12
+    eye = np.eye(64)
+    for h in range(4):
+        np.testing.assert_allclose(T1[h] @ (eye - A[h]), eye, atol=1e-10)
+
+
+def test_neumann_closed_form_small():
+    rng = np.random.default_rng(3)
+    C = 12
+    A = np.tril(rng.standard_normal((C, C)) * 0.3, -1)
+    series = np.eye(C)
+    P = np.eye(C)
+    for _ in range(C):
+        P = P @ A
+        series = series + P
+    np.testing.assert_allclose(og.inverse_fp64(A[None])[0], series, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(og.forward_subst(A), series, rtol=1e-10, atol=1e-12)
+
+
+def test_build_A_special_cases():
+    rng = np.random.default_rng(5)
+    k = rng.standard_normal((1, 8, 16))
+    gc = -np.abs(rng.standard_normal((1, 8)))
+    assert np.all(og.build_A(k, np.zeros((1, 8)), gc) == 0.0)
+    # orthogonal keys -> no interaction
+    ko = np.eye(8)[None, :, :8]
+    assert np.allclose(og.build_A(ko, np.ones((1, 8)), gc), 0.0)
+    # two tokens: A[1,0] = -beta_1 * cos(k0, k1) * exp(gc_1)
+    k2 = rng.standard_normal((2, 4))
+    b = np.array([0.3, 0.7])
+    g = np.array([-0.2, -0.5])
+    A = og.build_A(k2[None], b[None], g[None])[0]
+    cos = k2[0] @ k2[1] / np.sqrt((k2[0] @ k2[0] + 1e-6) * (k2[1] @ k2[1] + 1e-6))
+    assert A[0, 0] == 0 and A[0, 1] == 0 and A[1, 1] == 0
+    assert np.isclose(A[1, 0], -0.7 * cos * np.exp(-0.5))
+
+
+def test_oc_definition():
+    T = np.ones((2, 3, 3))
+    assert og.oc(T, T) == 0.0
+    assert np.isclose(og.oc(2 * T, T), 1.0)
+
+
+def test_u16_codes_roundtrip():
+    x = np.linspace(-1.5, 1.5, 101)
+    q = og.quantize_u16(x, og.ST_REF)
+    np.testing.assert_allclose(og.dequantize_u16(q, og.ST_REF), x, atol=og.ST_REF / 2 + 1e-15)
+
+
+def _int16_codes(A):
+    sA = float(np.abs(A).max() / 32767.0)
+    return np.clip(np.rint(A / sA), -32767, 32767).astype(np.int16), sA
+
+
+@pytest.mark.skipif(not (REF_DIR / "gdn_solve_ref").exists(), reason="oracle/_ref not built (needs /root/reference)")
+def test_int16_block_model_matches_reference_c(tmp_path):
+    k, beta, gc = og.config4_inputs(heads=3, C=64, seed=7)
+    A = og.build_A(k, beta, gc)
+    codes, sAs = [], []
+    for h in range(3):
+        q, s = _int16_codes(A[h])
+        codes.append(q)
+        sAs.append(s)
+    sT = 2.0 / 32767.0
+    np.array([3, 64], np.int32).tofile(tmp_path / "dims.i32")
+    np.stack(codes).astype(np.int16).tofile(tmp_path / "A_codes.i16")
+    np.array(sAs, np.float32).tofile(tmp_path / "sA.f32")
+    np.array([sT], np.float32).tofile(tmp_path / "sT.f32")
+    subprocess.run([str(REF_DIR / "gdn_solve_ref")], cwd=tmp_path, check=True, capture_output=True)
+    T_ref = np.fromfile(tmp_path / "T_out.f64", np.float64).reshape(3, 64, 64)
+    for h in range(3):
+        # the C model reads sA as float32 and sT as float32
+        T_py = og.solve_int16_blocks(codes[h], float(np.float32(sAs[h])), float(np.float32(sT)))
+        np.testing.assert_allclose(T_py, T_ref[h], rtol=0, atol=1e-12)
+        # and the model is a faithful inverse at its int16 precision
+        assert og.oc(T_py, og.inverse_fp64(codes[h].astype(np.float64) * np.float32(sAs[h]))) < 5e-4

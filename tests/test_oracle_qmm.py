@@ -1,0 +1,158 @@
+"""CPU tests: the matmul oracle and case generator against the reference's golden vectors,
+plus closed-form pins of the integer contracts."""
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import qmm
+from qcom_htp_amd import cases as C
+
+GOLD = Path(__file__).resolve().parent / "golden"
+SMALL = np.load(GOLD / "qmm_small.npz")
+SMALL_META = json.loads((GOLD / "qmm_small.json").read_text())
+GATE_META = json.loads((GOLD / "qmm_256.json").read_text())
+
+ALL_KEYS = sorted(SMALL_META)
+GATED_KEYS = [k for k in ALL_KEYS if k.split("/")[0] in C.GATED_FAMILIES]
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).reshape(-1).tobytes()).hexdigest()
+
+
+def test_golden_covers_all_families_and_cases():
+    fams = {k.split("/")[0] for k in SMALL_META}
+    cases = {k.split("/")[1] for k in SMALL_META}
+    assert fams == set(C.FAMILIES)
+    assert cases == set(C.CASES)
+    assert set(GATE_META) == set(SMALL_META)
+
+
+@pytest.mark.parametrize("key", ALL_KEYS)
+def test_seed_and_weight_quantizer_match_golden(key):
+    fam, case = key.split("/")
+    F = C.FAMILIES[fam]
+    assert C.seed_for(fam, case) == SMALL_META[key]["seed"]
+    _, w, _ = C.make_float_case(F, case, 32, 128, 32)
+    wq = C.quantize_weight(F, w)
+    np.testing.assert_array_equal(wq["q"], SMALL[key + "/weight_q_nk"])
+    assert wq["scale"].dtype == SMALL[key + "/weight_scale"].dtype
+    np.testing.assert_array_equal(wq["scale"], SMALL[key + "/weight_scale"])
+    if F.is_lpbq:
+        np.testing.assert_array_equal(wq["block_int_scale"], SMALL[key + "/weight_lpbq_per_block_int_scale"])
+        np.testing.assert_array_equal(wq["expanded"], SMALL[key + "/weight_lpbq_expanded_q_nk"])
+
+
+@pytest.mark.parametrize("key", GATED_KEYS)
+def test_case_and_oracle_match_golden_small(key):
+    fam, case = key.split("/")
+    c = C.make_case(fam, case, 32, 128, 32)
+    meta = SMALL_META[key]
+    assert float(c.act_scale).hex() == meta["act_scale"]
+    assert float(c.out_scale).hex() == meta["out_scale"]
+    for name, arr in (
+        ("activation_q", c.activation_q),
+        ("weight_q_nk", c.weight_q_nk),
+        ("bias_q_int32", c.bias_q),
+    ):
+        g = SMALL[key + "/" + name]
+        assert arr.dtype == g.dtype, name
+        np.testing.assert_array_equal(arr, g, err_msg=name)
+    out = qmm.expected_output_case(c)
+    g = SMALL[key + "/output_q"]
+    assert out.dtype == g.dtype
+    np.testing.assert_array_equal(out, g)
+    qr = qmm.dequantized_output(c.activation_q, c.weight_int_nk, c.weight_scale, c.bias_q, c.act_scale, c.family.act_zp)
+    np.testing.assert_array_equal(qr.astype(np.float32), SMALL[key + "/output_quantized_path_float"])
+
+
+@pytest.mark.parametrize("key", GATED_KEYS)
+def test_case_and_oracle_match_golden_256(key):
+    fam, case = key.split("/")
+    c = C.make_case(fam, case, 256, 256, 256)
+    meta = GATE_META[key]
+    assert float(c.act_scale).hex() == meta["act_scale"]
+    assert float(c.out_scale).hex() == meta["out_scale"]
+    digests = meta["sha256"]
+    assert sha(c.activation_q) == digests["activation_q"]
+    assert sha(c.weight_q_nk) == digests["weight_q_nk"]
+    assert sha(c.weight_scale) == digests["weight_scale"]
+    assert sha(c.bias_q) == digests["bias_q_int32"]
+    if c.lpbq_block_int_scale is not None:
+        assert sha(c.lpbq_block_int_scale) == digests["weight_lpbq_per_block_int_scale"]
+        assert sha(c.lpbq_expanded_q_nk) == digests["weight_lpbq_expanded_q_nk"]
+    out = qmm.expected_output_case(c)
+    assert sha(out) == digests["output_q"]
+
+
+def test_oracle_detects_planted_mistakes():
+    """A plausible slip (dropping fl32 rounding of w_deq, or of the zero point) changes outputs."""
+    c = C.make_case("w8a16", "normal_random", 256, 256, 256)
+    good = qmm.expected_output_case(c)
+    F = c.family
+    # variant 1: dequantise weights in float64 instead of the float32 product
+    bias_scale = c.act_scale * c.weight_scale.astype(np.float64)
+    x = (c.activation_q.astype(np.float64) - F.act_zp) * c.act_scale
+    w64 = c.weight_q_nk.astype(np.float64) * c.weight_scale.astype(np.float64)[:, None]
+    qr = x @ w64.T + c.bias_q * bias_scale
+    bad = np.clip(np.rint(qr / c.out_scale + F.out_zp), 0, F.out_qmax)
+    assert (bad != good).sum() > 0
+    # variant 2: forget the activation zero point
+    bad2 = qmm.expected_output(c.activation_q, c.weight_q_nk, c.weight_scale, c.bias_q, c.act_scale, c.out_scale, 0,
+                               F.out_zp, F.out_bits)
+    assert (bad2 != good).sum() > 1000
+
+
+def test_int_accumulator_bruteforce():
+    rng = np.random.default_rng(0)
+    a = rng.integers(0, 65536, size=(3, 64)).astype(np.uint16)
+    w = rng.integers(-127, 128, size=(5, 64)).astype(np.int8)
+    acc = qmm.int_accumulator(a, w, 32768)
+    brute = np.array([[sum((int(a[i, k]) - 32768) * int(w[j, k]) for k in range(64)) for j in range(5)] for i in range(3)])
+    np.testing.assert_array_equal(acc, brute)
+
+
+def test_reference_step_contracts():
+    rng = np.random.default_rng(1)
+    w = rng.integers(-7, 8, size=(64, 32)).astype(np.int32)  # [K, N]
+    bias = rng.integers(-50, 50, size=32).astype(np.int32)
+    # activations at the zero point: the accumulator vanishes -> legacy = clip(bias)
+    cur = np.full((4, 64), 128, np.uint8)
+    out = qmm.reference_step(8, 4, 8, cur, w, bias, "legacy")
+    np.testing.assert_array_equal(out, np.clip(bias, 0, 255)[None, :].repeat(4, 0))
+    # native A16 contract at the zero point -> output zero point 32768
+    cur16 = np.full((2, 64), 32768, np.uint16)
+    np.testing.assert_array_equal(qmm.reference_step(16, 4, 16, cur16, w, None, "native", "w4a16"), 32768)
+    # single-k impulse: acc = (a - zp) * w[k]; W4A16 floors to a multiple of 256 before /7
+    cur16 = np.full((1, 64), 32768, np.uint16)
+    cur16[0, 5] = 32768 + 1000
+    got = qmm.reference_step(16, 4, 16, cur16, w, None, "native", "w4a16")
+    acc = 1000 * w[5].astype(np.int64)
+    acc = (acc // 256) * 256
+    np.testing.assert_array_equal(got[0], np.clip(np.rint(acc / 7.0 + 32768), 0, 65535))
+    with pytest.raises(ValueError):
+        qmm.reference_step(8, 4, 8, cur, w, bias, "native")
+
+
+def test_round_div7_ties_and_signs():
+    v = np.array([0, 3, 4, 10, 11, -3, -4, -10, -11, 7 * 1000 + 3, 7 * 1000 + 4, -(7 * 1000 + 4)])
+    expect = np.array([0, 0, 1, 1, 2, 0, -1, -1, -2, 1000, 1001, -1001])
+    np.testing.assert_array_equal(qmm.round_div7(v), expect)
+
+
+def test_w4a8_lpbq_scalar_effective_bias():
+    rng = np.random.default_rng(2)
+    w = rng.integers(-7, 8, size=(64, 32))
+    act = np.full((2, 64), 128, np.uint8)
+    eff = -128 * w.sum(0) + 17
+    np.testing.assert_array_equal(qmm.w4a8_lpbq_scalar(eff, w, act), 17)
+
+
+def test_w4a16_lpbq_native_zero_point():
+    w = np.ones((64, 8), np.int64)
+    act = np.full((1, 64), 32768, np.uint16)
+    np.testing.assert_array_equal(qmm.w4a16_lpbq_scalar_native(act, w), 32768)

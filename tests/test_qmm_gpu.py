@@ -1,0 +1,139 @@
+"""GPU parity of the quantized matmul family: HIP kernels vs the reference's oracle.
+
+Bar: bit-exact.  The 7 named cases x 6 gated families at 256^3 are compared against the
+sha256 of the reference generator's own ``output_ref_q`` (tests/golden/qmm_256.json); the
+32x128x32 cases against the full golden arrays; other shapes against the oracle restatement
+(itself pinned to the golden vectors by tests/test_oracle_qmm.py).
+"""
+
+import hashlib
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import qmm as oq
+from qcom_htp_amd import cases as C
+
+pytestmark = pytest.mark.gpu
+
+GOLD = Path(__file__).resolve().parent / "golden"
+GATE_META = json.loads((GOLD / "qmm_256.json").read_text())
+SMALL = np.load(GOLD / "qmm_small.npz")
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).reshape(-1).tobytes()).hexdigest()
+
+
+def run(case, gpu, path=0, rows=None):
+    import torch
+
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    op = QuantMatmul.from_case(case, device=gpu)
+    act = case.activation_q if rows is None else case.activation_q[:rows]
+    a = torch.from_numpy(np.ascontiguousarray(act)).to(gpu)
+    out = op(a, path=path)
+    torch.cuda.synchronize()
+    res = out.cpu().numpy()
+    op.close()
+    return res
+
+
+def diff_msg(got, want):
+    bad = np.argwhere(got.astype(np.int64) != want.astype(np.int64))
+    if bad.size == 0:
+        return "identical"
+    i, j = bad[0]
+    return f"{len(bad)} mismatches, first at {tuple(bad[0])}: got {got[i, j]} want {want[i, j]}"
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+@pytest.mark.parametrize("case", C.CASES)
+def test_gemm_seven_cases_256_bit_exact(gpu, fam, case):
+    c = C.make_case(fam, case, 256, 256, 256)
+    print(f"[qmm] {fam}/{case} 256^3 gemm", flush=True)
+    got = run(c, gpu, path=1)
+    want_sha = GATE_META[f"{fam}/{case}"]["sha256"]["output_q"]
+    if sha(got) != want_sha:
+        pytest.fail(f"{fam}/{case}: {diff_msg(got, oq.expected_output_case(c))}")
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+@pytest.mark.parametrize("case", C.CASES)
+def test_small_cases_match_golden_arrays(gpu, fam, case):
+    c = C.make_case(fam, case, 32, 128, 32)
+    want = SMALL[f"{fam}/{case}/output_q"]
+    print(f"[qmm] {fam}/{case} 32x128x32 gemm", flush=True)
+    got = run(c, gpu, path=1)
+    assert got.dtype == want.dtype
+    assert np.array_equal(got, want), f"gemm: {diff_msg(got, want)}"
+    # the decode GEMV takes at most 16 rows per call: run both halves
+    print(f"[qmm] {fam}/{case} 32x128x32 gemv", flush=True)
+    for r0 in (0, 16):
+        sub = C.QmmCase(**{**c.__dict__, "activation_q": c.activation_q[r0:r0 + 16], "m": 16})
+        got = run(sub, gpu, path=2)
+        assert np.array_equal(got, want[r0:r0 + 16]), f"gemv rows {r0}..: {diff_msg(got, want[r0:r0 + 16])}"
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+@pytest.mark.parametrize("rows", [1, 3, 16])
+def test_gemv_decode_rows_bit_exact(gpu, fam, rows):
+    c = C.make_case(fam, "normal_random", 256, 256, 256)
+    print(f"[qmm] {fam} gemv rows={rows}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    want = oq.expected_output_case(c)[:rows]
+    assert np.array_equal(got, want), diff_msg(got, want)
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+def test_accumulators_exact(gpu, fam):
+    import torch
+
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    c = C.synthetic_case(fam, 96, 512, 160, seed=11, lpbq_block=32, lpbq_max_scale=16)
+    print(f"[qmm] {fam} accumulate 96x512x160", flush=True)
+    op = QuantMatmul.from_case(c, device=gpu)
+    acc = op.accumulate(torch.from_numpy(c.activation_q).to(gpu))
+    torch.cuda.synchronize()
+    want = oq.int_accumulator(c.activation_q, c.weight_int_nk, c.family.act_zp)
+    np.testing.assert_array_equal(acc.cpu().numpy(), want)
+    op.close()
+
+
+SHAPES = [(1, 256, 32), (17, 96, 64), (300, 1024, 480), (257, 512, 288), (64, 4096, 256)]
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+@pytest.mark.parametrize("mkn", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_synthetic_shapes_bit_exact(gpu, fam, mkn):
+    m, k, n = mkn
+    F = C.FAMILIES[fam]
+    if F.is_lpbq and k <= 64:
+        pytest.skip("LPBQ needs K > block size")
+    c = C.synthetic_case(fam, m, k, n, seed=m + k + n, lpbq_block=64 if k % 64 == 0 else 32)
+    want = oq.expected_output_case(c)
+    for path in ((1, 2) if m <= 16 else (1,)):
+        print(f"[qmm] {fam} synthetic {m}x{k}x{n} path={path}", flush=True)
+        got = run(c, gpu, path=path)
+        assert np.array_equal(got, want), f"path {path}: {diff_msg(got, want)}"
+
+
+def test_invalid_arguments_report_status(gpu):
+    import torch
+
+    from qcom_htp_amd import _lib
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    c = C.make_case("u8i8", "normal_random", 32, 128, 32)
+    op = QuantMatmul.from_case(c, device=gpu)
+    with pytest.raises(TypeError):
+        op(torch.zeros((4, 128), dtype=torch.uint16, device=gpu))
+    with pytest.raises(ValueError):
+        op(torch.zeros((4, 64), dtype=torch.uint8, device=gpu))
+    with pytest.raises(_lib.QhtpError):
+        op(torch.zeros((32, 128), dtype=torch.uint8, device=gpu), path=2)  # M=32 > 16 on the GEMV
+    op.close()
