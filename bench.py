@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the qcom_htp hot paths on one MI355X.
+
+Primary line (the driver contract): the W4A8 per-channel quantized GEMM at M=K=N=4096
+(uint8 activations ~ N(128, 40), int4 weights, per-channel fp32 scales, int32 bias, uint8
+output), one step = one full requantised GEMM.  ``value`` is TOPS (2*M*K*N per step).
+Extra figures in the same JSON line: W8A16 and u8i8 GEMMs at 4096^3, LPBQ GEMMs at
+4096x4096x14336, the M=1 / M=16 LPBQ GEMV in GB/s (weights rotated over > 256 MB so the
+MALL cannot serve them), and the GDN (I - A)^-1 solve at C=256 x 32 heads in heads/s.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+I8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA (5.0 POPS)
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_kernel(fn, steps: int, warmup: int):
+    """(ms per step, from host wall clock with syncs; ms per step from stream events)."""
+    import torch
+
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        fn(i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = start.elapsed_time(stop) / steps
+    return wall, ev
+
+
+def gemm_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, check_rows: int = 0,
+                  lpbq_block: int = 64):
+    import numpy as np
+    import torch
+
+    from qcom_htp_amd import cases
+    from qcom_htp_amd.qmm import PATH_GEMM, QuantMatmul
+
+    dev = torch.device("cuda", 0)
+    case = cases.synthetic_case(family, m, k, n, seed=2, lpbq_block=lpbq_block)
+    op = QuantMatmul.from_case(case, device=dev)
+    act = torch.from_numpy(case.activation_q).to(dev)
+    out = torch.empty((m, n), dtype=op.out_dtype, device=dev)
+    wall, ev = time_kernel(lambda i: op(act, out=out, path=PATH_GEMM), steps, warmup)
+    ops = 2.0 * m * k * n
+    res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "tops": ops / (ev * 1e-3) / 1e12}
+    if check_rows:
+        from oracle import qmm as oq  # parity spot check only
+
+        sub = cases.QmmCase(**{**case.__dict__, "activation_q": case.activation_q[:check_rows], "m": check_rows})
+        want = oq.expected_output_case(sub)
+        got = out[:check_rows].cpu().numpy()
+        res["parity_rows_checked"] = check_rows
+        res["parity_mismatches"] = int((got.astype(np.int64) != want.astype(np.int64)).sum())
+    op.close()
+    return res, case
+
+
+def gemv_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, copies: int, lpbq_block: int = 64):
+    import torch
+
+    from qcom_htp_amd import cases
+    from qcom_htp_amd.qmm import PATH_GEMV, QuantMatmul
+
+    dev = torch.device("cuda", 0)
+    case = cases.synthetic_case(family, m, k, n, seed=3, lpbq_block=lpbq_block)
+    ops = [QuantMatmul.from_case(case, device=dev) for _ in range(copies)]
+    act = torch.from_numpy(case.activation_q).to(dev)
+    out = torch.empty((m, n), dtype=ops[0].out_dtype, device=dev)
+    wall, ev = time_kernel(lambda i: ops[i % copies](act, out=out, path=PATH_GEMV), steps, warmup)
+    info = ops[0].info
+    act_b = m * k * (2 if family.endswith("a16") or "a16" in family else 1)
+    out_b = m * n * (2 if "a16" in family else 1)
+    per_ch = n * (4 + 4)  # fp32 scale + int32 bias (the reference's per-channel operands)
+    nbytes = info["gemv_weight_bytes"] + per_ch + act_b + out_b
+    res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "bytes": nbytes,
+           "gbs": nbytes / (ev * 1e-3) / 1e9, "weight_copies": copies,
+           "rotated_mb": copies * info["gemv_weight_bytes"] / 1e6}
+    for o in ops:
+        o.close()
+    return res
+
+
+def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
+    import numpy as np
+    import torch
+
+    from qcom_htp_amd.gdn import gdn_solve
+
+    rng = np.random.default_rng(4)
+    k = rng.standard_normal((heads, C, 128))
+    k /= np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((heads, C))))
+    g = np.cumsum(-np.logaddexp(0.0, -(rng.standard_normal((heads, C)) + 3.0)), axis=-1)
+    low = np.tril(np.ones((C, C), bool), -1)
+    A = np.where(low, -(beta[:, :, None] * (k @ k.transpose(0, 2, 1))) * np.exp(g[:, :, None] - g[:, None, :]), 0.0)
+    dev = torch.device("cuda", 0)
+    a = torch.from_numpy(A.astype(np.float32)).to(dev)
+    out = torch.empty_like(a)
+    wall, ev = time_kernel(lambda i: gdn_solve(a, precision=precision, out=out), steps, warmup)
+    flops = (2.0 / 3.0) * C ** 3 * heads
+    return {"heads": heads, "C": C, "precision": "fp32" if precision == 0 else "bf16", "ms": ev, "wall_ms": wall,
+            "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12}, A
+
+
+def cpu_baseline(case, gdn_A):
+    """The oracle (numpy/LAPACK restatement of the reference's CPU path) on host cores."""
+    import numpy as np
+
+    from oracle import gdn as og
+    from oracle import qmm as oq
+    from qcom_htp_amd import cases
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"), default=1)
+    except Exception:  # pragma: no cover
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    rows = 1024
+    sub = cases.QmmCase(**{**case.__dict__, "activation_q": case.activation_q[:rows], "m": rows})
+    oq.expected_output_case(cases.QmmCase(**{**case.__dict__, "activation_q": case.activation_q[:64], "m": 64}))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oq.expected_output_case(sub)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    ops = 2.0 * rows * case.k * case.n
+    g_heads = 8
+    t0 = time.perf_counter()
+    og.inverse_fp64(gdn_A[:g_heads])
+    tg = time.perf_counter() - t0
+    return {
+        "value": ops / t / 1e12,
+        "unit": "TOPS",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"oracle output_ref_q (float64 dgemm + requant) on {rows} of {case.m} rows of the "
+                  f"{case.k}x{case.n} W4A8 case, median of 3",
+        "gdn_heads_per_s": g_heads / tg,
+        "gdn_sample": f"np.linalg.inv(I - A) float64 on {g_heads} heads of C={gdn_A.shape[-1]}",
+        "affinity_cpus": len(os.sched_getaffinity(0)),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="primary line only (no extras, no CPU baseline)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (no multi-GPU path); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    torch.cuda.init()
+
+    M = K = N = 4096
+    log("primary: w4a8_per_channel GEMM 4096^3")
+    prim, case = gemm_workload("w4a8_per_channel", M, K, N, args.steps, args.warmup, check_rows=64)
+    extra = {"w4a8_gemm_4096": prim}
+    gdn_A = None
+    if not args.quick:
+        for fam in ("w8a16", "u8i8", "w4a16_per_channel"):
+            log(f"gemm {fam} 4096^3")
+            extra[f"{fam}_gemm_4096"] = gemm_workload(fam, M, K, N, max(5, args.steps // 2), 2)[0]
+        for fam in ("w4a8_lpbq", "w4a16_lpbq"):
+            log(f"gemm {fam} 4096x4096x14336")
+            extra[f"{fam}_gemm_4096x14336"] = gemm_workload(fam, 4096, 4096, 14336, 5, 2)[0]
+        for fam in ("w4a8_lpbq", "w4a16_lpbq"):
+            for m in (1, 16):
+                log(f"gemv {fam} M={m} 4096x14336")
+                extra[f"{fam}_gemv_m{m}"] = gemv_workload(fam, m, 4096, 14336, 200, 20, copies=10)
+        for prec in (0, 1):
+            log(f"gdn C=256 x 32 heads precision={prec}")
+            r, gdn_A = gdn_workload(32, 256, 50, 5, prec)
+            extra[f"gdn_c256_h32_{r['precision']}"] = r
+    torch.cuda.synchronize()
+
+    tops = prim["tops"]
+    line = {
+        "metric": "W4A8/W8A16 GEMM TOPS (% i8 MFMA peak) @4096³; GDN (I−A)⁻¹ heads/s @C=256",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(prim["wall_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "w4a8_per_channel quantized GEMM, u8 act x int4 weight -> u8, M=K=N=4096",
+                   "m": M, "k": K, "n": N, "family": "w4a8_per_channel"},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": I8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": round(tops / I8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "qmm_gemm_kernel<A8, int4 tiles>", "measured": "stream events over the timed steps"},
+        "extra": extra,
+    }
+    if not args.quick:
+        log("cpu baseline (oracle on host cores)")
+        line["cpu_baseline"] = cpu_baseline(case, gdn_A)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

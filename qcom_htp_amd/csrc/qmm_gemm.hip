@@ -12,12 +12,17 @@
 //   * int4 weights (offset-binary nibbles) are widened to int8 in registers, and LPBQ
 //     block scales are applied there too: (u*f + 128 - 8f) ^ 0x80 per byte is the two's
 //     complement of (u - 8) * f with no carry between bytes.
-// Epilogue: the exact integer dot product S (int32 MFMA accumulators, combined in int64 for
-// 16-bit activations) is requantised in float64 as t = S*alpha + beta; rint(t) is certain
-// unless t lies within the per-channel margin of a rounding boundary, in which case the
-// element is queued in LDS and recomputed after the tile by a wave-cooperative float64 dot
-// product that forms every term exactly as the reference oracle does
+// Epilogue: the accumulators are staged through the (then idle) LDS in two halves, so each
+// thread requantises one output channel down a column of rows with coalesced stores.  The
+// exact integer dot product S (int32 MFMA accumulators, combined in int64 for 16-bit
+// activations) becomes t = S*alpha + beta in float64; rint(t) is certain unless t lies within
+// the per-channel margin of a rounding boundary, in which case the element is queued in LDS
+// and recomputed after the tile by a wave-cooperative float64 dot product that forms every
+// term exactly as the reference oracle does
 // (scripts/generate_qnn_matmul_python_cases.py:472-481).
+
+#include <type_traits>
+#include <utility>
 
 #include "qmm_internal.h"
 
@@ -26,6 +31,16 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Compile-time loop: f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 struct GemmArgs {
   const uint8_t *act;
@@ -39,6 +54,12 @@ struct GemmArgs {
   int act_zp, out_zp, out_qmax, out16;
   double sA, sO;
 };
+
+// LDS arena: two pipeline stages of (A tile, B tile), 32 KiB each; the epilogue reuses it to
+// stage half of the accumulator tile (128 rows x 256 cols int32, row stride padded to 260).
+constexpr int kStageU4 = kBM * kBK / 16;      // uint4 per operand tile
+constexpr int kEpiStride = 260;               // int32 per staged accumulator row (A8)
+constexpr int kArenaU4 = 4 * kStageU4 > 128 * kEpiStride / 4 ? 4 * kStageU4 : 128 * kEpiStride / 4;
 
 // Row-dependent XOR swizzle of the eight 16-byte chunks of a 128-byte LDS row: conflict-free
 // for the MFMA fragment reads (32 consecutive rows, same logical chunk) whether the LDS serves
@@ -54,12 +75,16 @@ __device__ __forceinline__ uint32_t widen4(uint32_t x, uint32_t f, uint32_t bias
   return (x * f + bias) ^ 0x80808080u;
 }
 
-__device__ __forceinline__ void store_u8(void *out, size_t idx, int v) { static_cast<uint8_t *>(out)[idx] = static_cast<uint8_t>(v); }
-__device__ __forceinline__ void store_u16(void *out, size_t idx, int v) { static_cast<uint16_t *>(out)[idx] = static_cast<uint16_t>(v); }
+__device__ __forceinline__ void store_out(void *out, int out16, size_t idx, int v) {
+  if (out16)
+    static_cast<uint16_t *>(out)[idx] = static_cast<uint16_t>(v);
+  else
+    static_cast<uint8_t *>(out)[idx] = static_cast<uint8_t>(v);
+}
 
 // Loads 16 consecutive weight codes (k .. k+15, k % 16 == 0) of operand column cb.
 template <int TFMT, bool LPBQ>
-__device__ __forceinline__ void load_w16(const GemmArgs &g, int cb, int k, int (&w)[16]) {
+__device__ __forceinline__ void load_w16(const GemmArgs g, int cb, int k, int (&w)[16]) {
   const size_t tile = static_cast<size_t>(cb / kBN) * g.KT + k / kBK;
   if (TFMT == kTileI8) {
     const int8_t *p = reinterpret_cast<const int8_t *>(g.tiles) + tile * (kBN * kBK) + (cb % kBN) * kBK + (k % kBK);
@@ -84,7 +109,7 @@ __device__ __forceinline__ void load_w16(const GemmArgs &g, int cb, int k, int (
 // Exact float64 recomputation of one output, term by term as the oracle forms it:
 // sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), then + bias_deq, / sO, + out_zp, rint, clip.
 template <bool A16, int TFMT, bool LPBQ>
-__device__ void fixup_one(const GemmArgs &g, int m, int n, int lane) {
+__device__ __noinline__ void fixup_one(const GemmArgs g, int m, int n, int lane) {
   const int cb = A16 ? (n / 32) * 64 + (n % 32) : n;
   const float sc = g.s32[n];
   double s = 0.0;
@@ -120,13 +145,8 @@ __device__ void fixup_one(const GemmArgs &g, int m, int n, int lane) {
   if (lane == 0) {
     const double qr = s + g.bias_deq[n];
     const double t = qr / g.sO + static_cast<double>(g.out_zp);
-    double o = rint(t);
-    o = fmin(fmax(o, 0.0), static_cast<double>(g.out_qmax));
-    const size_t idx = static_cast<size_t>(m) * g.N + n;
-    if (g.out16)
-      store_u16(g.out, idx, static_cast<int>(o));
-    else
-      store_u8(g.out, idx, static_cast<int>(o));
+    const double o = fmin(fmax(rint(t), 0.0), static_cast<double>(g.out_qmax));
+    store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, static_cast<int>(o));
   }
 }
 
@@ -147,9 +167,8 @@ __device__ __forceinline__ int requant(double S, double alpha, double beta, doub
 
 // MODE 0: requantised output; MODE 1: exact int64 accumulators sum_k (a - zp) * w_int.
 template <bool A16, int TFMT, bool LPBQ, int MODE>
-__global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
-  __shared__ uint4 lds_a[2][kBM * kBK / 16];
-  __shared__ uint4 lds_b[2][kBN * kBK / 16];
+__global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArgs g) {
+  __shared__ uint4 arena[kArenaU4];
   __shared__ uint32_t fix_list[kFixCap];
   __shared__ int fix_cnt;
 
@@ -160,12 +179,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
   const int m0 = blockIdx.y * rows_real;
   const int c0 = blockIdx.x * kBN;
   const int n0 = blockIdx.x * cols_real;
+  const int M = g.M, K = g.K, KT = g.KT;
+  const uint8_t *const act = g.act;
+  const uint8_t *const tiles_base = g.tiles + static_cast<size_t>(blockIdx.x) * KT * (TFMT == kTileI8 ? kBN * kBK : kBN * kBK / 2);
   if (t == 0) fix_cnt = 0;
 
   constexpr int NB = TFMT == kTileI8 ? 8 : 4;
   uint4 ra[8];
   uint4 rb[NB];
   uint32_t rf[NB];
+
+  auto lds_a = [&](int st) { return arena + (2 * st) * kStageU4; };
+  auto lds_b = [&](int st) { return arena + (2 * st + 1) * kStageU4; };
 
   auto load_a = [&](int kt) {
     if (!A16) {
@@ -174,8 +199,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int row = m0 + i * 32 + rr;
-        if (row < g.M && k < g.K)
-          ra[i] = *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(row) * g.K + k);
+        if (row < M && k < K)
+          ra[i] = *reinterpret_cast<const uint4 *>(act + static_cast<size_t>(row) * K + k);
         else
           ra[i] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
       }
@@ -185,14 +210,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int row = m0 + i * 16 + rr;
-        if (row < g.M && k < g.K)
-          ra[i] = *reinterpret_cast<const uint4 *>(g.act + (static_cast<size_t>(row) * g.K + k) * 2);
+        if (row < M && k < K)
+          ra[i] = *reinterpret_cast<const uint4 *>(act + (static_cast<size_t>(row) * K + k) * 2);
         else
           ra[i] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
       }
     }
   };
   auto store_a = [&](int st) {
+    uint4 *la = lds_a(st);
     if (!A16) {
       const int c = t & 7, rr = t >> 3;
 #pragma unroll
@@ -203,11 +229,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
         v.y ^= 0x80808080u;
         v.z ^= 0x80808080u;
         v.w ^= 0x80808080u;
-        lds_a[st][row * 8 + (c ^ swz(row))] = v;
+        la[row * 8 + (c ^ swz(row))] = v;
       }
     } else {
       const int c = t & 15, rr = t >> 4;
-      uint2 *l2 = reinterpret_cast<uint2 *>(lds_a[st]);
+      uint2 *l2 = reinterpret_cast<uint2 *>(la);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         uint4 v = ra[i];
@@ -226,12 +252,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
   };
   auto load_b = [&](int kt) {
     if (TFMT == kTileI8) {
-      const uint4 *base = reinterpret_cast<const uint4 *>(g.tiles + (static_cast<size_t>(blockIdx.x) * g.KT + kt) * (kBN * kBK));
+      const uint4 *base = reinterpret_cast<const uint4 *>(tiles_base + static_cast<size_t>(kt) * (kBN * kBK));
 #pragma unroll
       for (int i = 0; i < 8; ++i) rb[i] = base[i * 256 + t];
     } else {
-      const uint4 *base =
-          reinterpret_cast<const uint4 *>(g.tiles + (static_cast<size_t>(blockIdx.x) * g.KT + kt) * (kBN * kBK / 2));
+      const uint4 *base = reinterpret_cast<const uint4 *>(tiles_base + static_cast<size_t>(kt) * (kBN * kBK / 2));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         rb[i] = base[i * 256 + t];
@@ -246,12 +271,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
     }
   };
   auto store_b = [&](int st) {
+    uint4 *lb = lds_b(st);
     if (TFMT == kTileI8) {
       const int c = t & 7, cc = t >> 3;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int col = i * 32 + cc;
-        lds_b[st][col * 8 + (c ^ swz(col))] = rb[i];
+        lb[col * 8 + (c ^ swz(col))] = rb[i];
       }
     } else {
       const int c4 = t & 3, cc = t >> 2;
@@ -272,17 +298,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
         g1.z = widen4((v.z >> 4) & m4, f, bias);
         g1.w = widen4((v.w >> 4) & m4, f, bias);
         const int s = swz(col);
-        lds_b[st][col * 8 + ((2 * c4) ^ s)] = g0;
-        lds_b[st][col * 8 + ((2 * c4 + 1) ^ s)] = g1;
+        lb[col * 8 + ((2 * c4) ^ s)] = g0;
+        lb[col * 8 + ((2 * c4 + 1) ^ s)] = g1;
       }
     }
   };
 
   v16i acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{};
+  static_for<4>([&](auto i) { static_for<4>([&](auto j) { acc[i][j] = v16i{}; }); });
 
   load_a(0);
   load_b(0);
@@ -290,34 +313,34 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
   store_b(0);
   __syncthreads();
 
-  for (int kt = 0; kt < g.KT; ++kt) {
+  for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
-    const bool more = kt + 1 < g.KT;
+    const bool more = kt + 1 < KT;
     if (more) {
       load_a(kt + 1);
       load_b(kt + 1);
     }
+    const uint4 *la = lds_a(cur);
+    const uint4 *lb = lds_b(cur);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int ch = 2 * kk + (lane >> 5);
       v4i af[4], bf[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      static_for<4>([&](auto mt) {
         const int row = wm * 128 + mt * 32 + (lane & 31);
-        const uint4 v = lds_a[cur][row * 8 + (ch ^ swz(row))];
+        const uint4 v = la[row * 8 + (ch ^ swz(row))];
         af[mt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-      }
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+      });
+      static_for<4>([&](auto nt) {
         const int col = wn * 128 + nt * 32 + (lane & 31);
-        const uint4 v = lds_b[cur][col * 8 + (ch ^ swz(col))];
+        const uint4 v = lb[col * 8 + (ch ^ swz(col))];
         bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
+      });
+      static_for<4>([&](auto mt) {
+        static_for<4>([&](auto nt) {
           acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
+        });
+      });
     }
     if (more) {
       store_a(cur ^ 1);
@@ -327,22 +350,47 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
   }
 
   // ---------------------------------------------------------------- epilogue
-  if (!A16) {
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int n = n0 + wn * 128 + nt * 32 + (lane & 31);
-      if (n >= g.N) continue;
-      const double alpha = MODE == 0 ? g.alpha[n] : 0.0, beta = MODE == 0 ? g.beta[n] : 0.0;
-      const double margin = MODE == 0 ? g.margin[n] : 0.0, absb = MODE == 0 ? g.absb[n] : 0.0;
-      const int64_t corr = g.corr[n];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int rl = wm * 128 + mt * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+  int32_t *stage = reinterpret_cast<int32_t *>(arena);
+  static_for<2>([&](auto h) {
+    // 1) this wave's MFMA blocks mt = 2h, 2h+1 -> LDS
+    static_for<2>([&](auto mh) {
+      constexpr int mt = 2 * decltype(h)::value + decltype(mh)::value;
+      static_for<4>([&](auto nt) {
+        static_for<16>([&](auto j) {
+          const int qrow = mh * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);  // 0..63 within the half
+          const int col = nt * 32 + (lane & 31);
+          const int v = acc[mt][nt][j()];
+          if (!A16) {
+            stage[(wm * 64 + qrow) * kEpiStride + wn * 128 + col] = v;
+          } else {
+            // real row wm*32 + qrow/2, real column wn*64 + (nt/2)*32 + lane%32,
+            // component (column plane q|r) * 2 + (row plane hi|lo)
+            const int rr = wm * 32 + (qrow >> 1);
+            const int rc = wn * 64 + (nt >> 1) * 32 + (lane & 31);
+            const int comp = (nt & 1) * 2 + (qrow & 1);
+            stage[(rr * 128 + rc) * 4 + comp] = v;
+          }
+        });
+      });
+    });
+    __syncthreads();
+    // 2) requantise: one output channel per thread
+    if (!A16) {
+      const int n = n0 + t;
+      if (n < g.N) {
+        double alpha = 0, beta = 0, margin = 0, absb = 0;
+        if (MODE == 0) {
+          alpha = g.alpha[n];
+          beta = g.beta[n];
+          margin = g.margin[n];
+          absb = g.absb[n];
+        }
+        const int64_t corr = g.corr[n];
+        for (int r = 0; r < 128; ++r) {
+          const int rl = (r >> 6) * 128 + 64 * h + (r & 63);
           const int m = m0 + rl;
-          if (m >= g.M) continue;
-          const int64_t S = static_cast<int64_t>(acc[mt][nt][j]) + corr;
+          if (m >= M) continue;
+          const int64_t S = static_cast<int64_t>(stage[r * kEpiStride + t]) + corr;
           const size_t idx = static_cast<size_t>(m) * g.N + n;
           if (MODE == 1) {
             reinterpret_cast<int64_t *>(g.out)[idx] = S;
@@ -352,58 +400,53 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
           const int o = requant(static_cast<double>(S), alpha, beta, margin, absb, g.out_qmax, &amb);
           if (amb) {
             const int slot = atomicAdd(&fix_cnt, 1);
-            if (slot < kFixCap) fix_list[slot] = (static_cast<uint32_t>(rl) << 16) | static_cast<uint32_t>(n - n0);
-          } else if (g.out16) {
-            store_u16(g.out, idx, o);
+            if (slot < kFixCap) fix_list[slot] = (static_cast<uint32_t>(rl) << 16) | static_cast<uint32_t>(t);
           } else {
-            store_u8(g.out, idx, o);
+            store_out(g.out, g.out16, idx, o);
           }
         }
       }
-    }
-  } else {
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int n = n0 + wn * 64 + p * 32 + (lane & 31);
-      if (n >= g.N) continue;
-      const double alpha = MODE == 0 ? g.alpha[n] : 0.0, beta = MODE == 0 ? g.beta[n] : 0.0;
-      const double margin = MODE == 0 ? g.margin[n] : 0.0, absb = MODE == 0 ? g.absb[n] : 0.0;
-      const int64_t corr = g.corr[n], Mn = g.mant[n];
-      const int64_t csum = MODE == 1 ? g.colsum[n] * static_cast<int64_t>(128 + 32768 - g.act_zp) : 0;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          const int orow = wm * 128 + mt * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
-          const int rl = orow >> 1;
+    } else {
+      const int rc = t & 127, r0 = t >> 7;
+      const int n = n0 + rc;
+      if (n < g.N) {
+        double alpha = 0, beta = 0, margin = 0, absb = 0;
+        if (MODE == 0) {
+          alpha = g.alpha[n];
+          beta = g.beta[n];
+          margin = g.margin[n];
+          absb = g.absb[n];
+        }
+        const int64_t corr = g.corr[n], Mn = g.mant[n];
+        const int64_t csum = MODE == 1 ? g.colsum[n] * static_cast<int64_t>(128 + 32768 - g.act_zp) : 0;
+        for (int rr = r0; rr < 64; rr += 2) {
+          const int rl = (rr >> 5) * 64 + 32 * h + (rr & 31);
           const int m = m0 + rl;
-          if (m >= g.M) continue;
-          const int64_t xhq = acc[mt][2 * p][j], xlq = acc[mt][2 * p][j + 1];
-          const int64_t yhr = acc[mt][2 * p + 1][j], ylr = acc[mt][2 * p + 1][j + 1];
+          if (m >= M) continue;
+          const int4 v = *reinterpret_cast<const int4 *>(&stage[(rr * 128 + rc) * 4]);
+          // v.x = hi*q, v.y = lo*q, v.z = hi*r, v.w = lo*r
           const size_t idx = static_cast<size_t>(m) * g.N + n;
           if (MODE == 1) {
-            reinterpret_cast<int64_t *>(g.out)[idx] = 256 * xhq + xlq + csum;
+            reinterpret_cast<int64_t *>(g.out)[idx] = 256 * static_cast<int64_t>(v.x) + v.y + csum;
             continue;
           }
-          const int64_t S = 256 * (Mn * xhq + yhr) + Mn * xlq + ylr + corr;
+          const int64_t S = 256 * (Mn * v.x + v.z) + Mn * v.y + v.w + corr;
           bool amb;
           const int o = requant(static_cast<double>(S), alpha, beta, margin, absb, g.out_qmax, &amb);
           if (amb) {
             const int slot = atomicAdd(&fix_cnt, 1);
-            if (slot < kFixCap) fix_list[slot] = (static_cast<uint32_t>(rl) << 16) | static_cast<uint32_t>(n - n0);
-          } else if (g.out16) {
-            store_u16(g.out, idx, o);
+            if (slot < kFixCap) fix_list[slot] = (static_cast<uint32_t>(rl) << 16) | static_cast<uint32_t>(rc);
           } else {
-            store_u8(g.out, idx, o);
+            store_out(g.out, g.out16, idx, o);
           }
         }
       }
     }
-  }
+    __syncthreads();
+  });
   if (MODE == 1) return;
 
   // ---------------------------------------------------------------- exact fixup
-  __syncthreads();
   const int cnt = fix_cnt;
   if (cnt == 0) return;
   const bool full = cnt > kFixCap;  // list overflowed: recompute the whole tile exactly
@@ -419,7 +462,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(GemmArgs g) {
       c = static_cast<int>(v & 0xFFFFu);
     }
     const int m = m0 + r, n = n0 + c;
-    if (m >= g.M || n >= g.N) continue;
+    if (m >= M || n >= g.N) continue;
     fixup_one<A16, TFMT, LPBQ>(g, m, n, lane);
   }
 }

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(kGemvThreads) void qmm_gemv_kernel(GemvArgs g) {
       if (LPBQ) f = g.lpbq[(static_cast<size_t>(grp) * g.nblk + ((kg * 32) >> g.bs_shift)) * 16 + col];
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
-        if (m >= M) break;
+        if (MM == 1 || m < M) {  // predicated: MM is a compile-time trip count
         const uint4 *ap = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(m) * K + kg * 32);
         const uint4 a0 = ap[0], a1 = ap[1];
         int d = 0;
@@ -198,6 +198,7 @@ __global__ __launch_bounds__(kGemvThreads) void qmm_gemv_kernel(GemvArgs g) {
           e = __builtin_amdgcn_sdot4(static_cast<int>(b1.z), static_cast<int>(w[6]), e, false);
           e = __builtin_amdgcn_sdot4(static_cast<int>(b1.w), static_cast<int>(w[7]), e, false);
           acc2[m] += LPBQ ? e * f : e;
+        }
         }
       }
     }
@@ -227,7 +228,6 @@ __global__ __launch_bounds__(kGemvThreads) void qmm_gemv_kernel(GemvArgs g) {
       }
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
-        if (m >= M) break;
         const int64_t S = A16 ? 256 * static_cast<int64_t>(acc[m]) + acc2[m] + corr : static_cast<int64_t>(acc[m]) + corr;
         const double t = fma(static_cast<double>(S), alpha, beta);
         const double fl = floor(t);
@@ -235,16 +235,16 @@ __global__ __launch_bounds__(kGemvThreads) void qmm_gemv_kernel(GemvArgs g) {
         const bool near_tie = fabs((t - fl) - 0.5) <= slack;
         const double lo = fmin(fmax(fl, 0.0), static_cast<double>(g.out_qmax));
         const double hi = fmin(fmax(fl + 1.0, 0.0), static_cast<double>(g.out_qmax));
-        if (near_tie && lo != hi) {
-          amb_mask |= 1u << m;
-          continue;
+        const bool amb = near_tie && lo != hi;
+        if (m < M && amb) amb_mask |= 1u << m;
+        if (m < M && !amb) {
+          const double o = fmin(fmax(rint(t), 0.0), static_cast<double>(g.out_qmax));
+          const size_t idx = static_cast<size_t>(m) * g.N + n;
+          if (g.out16)
+            static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(o);
+          else
+            static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(o);
         }
-        const double o = fmin(fmax(rint(t), 0.0), static_cast<double>(g.out_qmax));
-        const size_t idx = static_cast<size_t>(m) * g.N + n;
-        if (g.out16)
-          static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(o);
-        else
-          static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(o);
       }
     }
     // exact fixup of ambiguous outputs, one wave-cooperative dot product each
