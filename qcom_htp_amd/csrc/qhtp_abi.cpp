@@ -109,7 +109,8 @@ qh_status qh_qmm_release(qh_qmm_prepared *prep) {
   hipError_t err = hipDeviceSynchronize();
   QmmDevice &D = prep->dev;
   void *ptrs[] = {D.tiles, D.lpbq_tiles, D.gemv_tiles, D.gemv_lpbq, D.alpha, D.beta, D.corr,
-                  D.margin, D.absb, D.bias_deq, D.s32, D.mant, D.colsum, D.gemv_margin_r1};
+                  D.margin, D.absb, D.bias_deq, D.s32, D.mant, D.colsum, D.gemv_margin_r1,
+                  D.colsum_r, D.alpha_e, D.expo};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   (void)hipSetDevice(cur);

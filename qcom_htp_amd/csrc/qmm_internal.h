@@ -17,12 +17,30 @@ constexpr int kGemmThreads = 256;
 // Capacity of the per-workgroup list of outputs that need the exact fp64 fixup.
 constexpr int kFixCap = 1024;
 
-// Tile storage of the weight operand (the "B" operand of the MFMA):
-//   kTileI8 : int8 bytes, tile (nt, kt) = [256 cols][128 k] contiguous (32 KiB)
-//   kTileI4 : two int4 codes per byte, offset-binary (code + 8); tile = [256 cols][64 B]
-//             (16 KiB); inside a column's 64 B, each 16-k group is 8 bytes whose low nibble
-//             j holds k = j and high nibble holds k = j + 8.
+// Tile storage of the weight operand (the "B" operand of the MFMA).  A tile (nt, kt) covers
+// 256 operand columns x 128 k and is stored exactly as the GEMM keeps it in LDS, so the kernel
+// fills LDS with straight 16-byte direct-to-LDS copies:
+//   kTileI8 : 32 KiB; column c owns 128 B = eight 16-k chunks, chunk s at 16 * (s ^ swz8(c)).
+//   kTileI4 : 16 KiB; two int4 codes per byte, offset-binary (code + 8); column c owns 64 B =
+//             eight 16-k groups of 8 B, group s at 8 * (s ^ swz_i4(c)); inside a group byte j
+//             holds k = j in its low nibble and k = j + 8 in its high nibble.
+// LPBQ block scales for the GEMM: per tile [256 cols][4] bytes, entry j = the scale of the
+// 32-k chunk j of the tile (1 KiB per tile, also an LDS image).
 enum TileFormat : int { kTileI8 = 0, kTileI4 = 1 };
+
+// XOR swizzles that make the MFMA fragment reads bank-conflict free (32 consecutive rows or
+// columns reading the same logical chunk hit distinct banks for 8- or 16-lane LDS phases).
+__host__ __device__ inline int swz8(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
+__host__ __device__ inline int swz_i4(int col) { return (col >> 2) & 7; }
+__host__ __device__ inline int swz16(int row) { return row & 15; }
+
+// Byte offset of (operand column c, depth k) inside its tile.
+__host__ __device__ inline int tile_off_i8(int c, int k) {
+  return c * 128 + 16 * (((k & 127) >> 4) ^ swz8(c)) + (k & 15);
+}
+__host__ __device__ inline int tile_off_i4(int c, int k) {
+  return c * 64 + 8 * (((k & 127) >> 4) ^ swz_i4(c)) + (k & 7);  // nibble: (k & 8) ? high : low
+}
 
 // Everything the GEMM / GEMV kernels read, resident on the device.
 struct QmmDevice {
@@ -45,6 +63,9 @@ struct QmmDevice {
   float *s32;       // per-channel weight scale
   int64_t *mant;    // 16-bit acts: 24-bit mantissa M of s32 (s32 = M * 2^E)
   int64_t *colsum;  // sum_k w_int[n][k]
+  int64_t *colsum_r; // sum_k r[n][k] (float32 rounding residues of the dequantised weights)
+  double *alpha_e;  // sA * 2^E / sO: output LSB per unit of the exact integer dot product in 2^E units
+  int32_t *expo;    // E of s32 = M * 2^E
   double *gemv_margin_r1; // 16-bit acts GEMV: per-channel coefficient of R1[m] in the margin
 };
 

@@ -73,13 +73,13 @@ struct TileWriter {
   int KT;  // number of 128-deep k tiles
   void put(int c, int k, int v) {
     size_t tile = static_cast<size_t>(c / kBN) * KT + k / kBK;
-    int cc = c % kBN, kk = k % kBK;
+    int cc = c % kBN;
     if (fmt == kTileI8) {
-      buf[tile * (kBN * kBK) + static_cast<size_t>(cc) * kBK + kk] = static_cast<uint8_t>(static_cast<int8_t>(v));
+      buf[tile * (kBN * kBK) + tile_off_i8(cc, k)] = static_cast<uint8_t>(static_cast<int8_t>(v));
     } else {
-      size_t off = tile * (kBN * kBK / 2) + static_cast<size_t>(cc) * (kBK / 2) + (kk / 16) * 8 + (kk % 16) % 8;
+      size_t off = tile * (kBN * kBK / 2) + tile_off_i4(cc, k);
       uint8_t nib = static_cast<uint8_t>((v + 8) & 15);
-      if ((kk % 16) < 8)
+      if ((k & 8) == 0)
         buf[off] = static_cast<uint8_t>((buf[off] & 0xF0) | nib);
       else
         buf[off] = static_cast<uint8_t>((buf[off] & 0x0F) | (nib << 4));
@@ -220,10 +220,14 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
         tw.put(n, k, v);
       }
     if (gemm_lpbq_regs) {
-      const int nb = sh.Kp / bs;
-      lpbq_tiles.assign(static_cast<size_t>(sh.ncols_op) * nb, 1);
+      // per tile (nt, kt): [256 cols][4] -- the block scale of each 32-k chunk of the tile
+      lpbq_tiles.assign(static_cast<size_t>(sh.ncols_op / kBN) * KT * kBN * 4, 1);
       for (int n = 0; n < N; ++n)
-        for (int b = 0; b < nblk; ++b) lpbq_tiles[static_cast<size_t>(n) * nb + b] = d->lpbq_block_scale[static_cast<size_t>(n) * nblk + b];
+        for (int k32 = 0; k32 < K / 32; ++k32) {
+          const size_t tile = static_cast<size_t>(n / kBN) * KT + (k32 * 32) / kBK;
+          lpbq_tiles[tile * (kBN * 4) + (n % kBN) * 4 + (k32 & 3)] =
+              d->lpbq_block_scale[static_cast<size_t>(n) * nblk + (k32 * 32) / bs];
+        }
     }
   } else {
     for (int n = 0; n < N; ++n) {
@@ -268,7 +272,9 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   const double amax = static_cast<double>(std::max(d->act_zp, act_qmax - d->act_zp));
   const int Np = sh.Np;
   std::vector<double> alpha(Np, 0.0), beta(Np, 0.0), margin(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0), mr1(Np, 0.0);
-  std::vector<int64_t> corr(Np, 0), mantv(Np, 0), csum(Np, 0);
+  std::vector<int64_t> corr(Np, 0), mantv(Np, 0), csum(Np, 0), csum_r(Np, 0);
+  std::vector<double> alpha_e(Np, 0.0);
+  std::vector<int32_t> expov(Np, 0);
   std::vector<float> s32v(Np, 1.0f);
   const double a_base = a16 ? 32768.0 : 128.0;  // the kernels shift activations by this
   for (int n = 0; n < N; ++n) {
@@ -294,6 +300,9 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     absb[n] = 2.0 * std::fabs(beta[n]) + 2.0 * d->out_zp + 1.0;
     mantv[n] = mant[n];
     csum[n] = colsum_q[n];
+    csum_r[n] = colsum_r[n];
+    alpha_e[n] = sA * two_e / sO;
+    expov[n] = expo[n];
     s32v[n] = s;
   }
 
@@ -320,6 +329,9 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.s32, s32v);
   if (st == QH_STATUS_OK) st = al.upload(&D.mant, mantv);
   if (st == QH_STATUS_OK) st = al.upload(&D.colsum, csum);
+  if (st == QH_STATUS_OK) st = al.upload(&D.colsum_r, csum_r);
+  if (st == QH_STATUS_OK) st = al.upload(&D.alpha_e, alpha_e);
+  if (st == QH_STATUS_OK) st = al.upload(&D.expo, expov);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
   if (st != QH_STATUS_OK) {
     al.release();
