@@ -53,7 +53,8 @@ struct GemmArgs {
   const uint8_t *tiles;
   const uint8_t *lpbq;
   const double *alpha, *beta, *margin, *absb, *bias_deq;
-  const int64_t *corr, *mant, *colsum;
+  const double *alpha_e, *inv_pow2e, *margin_exact;
+  const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
   int M, N, K, KT, TM, TN;
   int act_zp, out_zp, out_qmax, out16;
@@ -200,7 +201,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   using C = Cfg<A16, TFMT, LPBQ>;
   __shared__ __attribute__((aligned(16))) uint8_t arena[C::kArena];
   __shared__ uint32_t fix_list[kFixCap];
-  __shared__ int fix_cnt;
+  __shared__ int fix_acc[A16 ? 1 : kFixCap];  // 8-bit acts: int32 accumulator of each listed output
+  __shared__ int fix_cnt, unc_cnt;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -214,7 +216,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const uint8_t *const act = g.act;
   const uint8_t *const btiles = g.tiles + static_cast<size_t>(tn) * KT * C::kTileB;
   const uint8_t *const ftiles = LPBQ ? g.lpbq + static_cast<size_t>(tn) * KT * C::kTileF : nullptr;
-  if (t == 0) fix_cnt = 0;
+  if (t == 0) {
+    fix_cnt = 0;
+    unc_cnt = 0;
+  }
 
   auto stage_a = [&](int st) { return arena + st * C::kStageBytes; };
   auto stage_b = [&](int st) { return arena + st * C::kStageBytes + kTileA; };
@@ -330,9 +335,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // Straight from the accumulator registers: each lane requantises the 4 rows x 1 column
   // strips of its MFMA blocks, then the 4 lanes of a quad transpose their strips (DPP quad
   // broadcasts + byte permutes) so every lane stores 4 adjacent outputs of one row.
-  auto push_fix = [&](int r, int c) {
+  auto push_fix = [&](int r, int c, int a) {
     const int slot = atomicAdd(&fix_cnt, 1);
-    if (slot < kFixCap) fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(c);
+    if (slot < kFixCap) {
+      fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(c);
+      if (!A16) fix_acc[slot] = a;
+    }
   };
   const int q = lane & 3;
   const double qmaxd = static_cast<double>(g.out_qmax);
@@ -367,7 +375,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             const double rd = rint(tv);
             int oi = static_cast<int>(rd);
             o[jj] = oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi);
-            if (fabs(tv - rd) > thr && tv > -1.0 && tv < qmaxd + 1.0 && nok && m0 + R + jj < M) push_fix(R + jj, cl);
+            if (fabs(tv - rd) > thr && tv > -1.0 && tv < qmaxd + 1.0 && nok && m0 + R + jj < M) push_fix(R + jj, cl, a);
           });
           if (MODE == 1) return;
           if (!g.out16) {
@@ -429,7 +437,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             int oi = static_cast<int>(rd);
             o[jj] = oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi);
             const double slack = margin + 0x1p-48 * (fabs(u) + fabs(tv) + absb);
-            if (fabs(tv - rd) > 0.5 - slack && tv > -1.0 && tv < qmaxd + 1.0 && nok && m0 + R + jj < M) push_fix(R + jj, cl);
+            if (fabs(tv - rd) > 0.5 - slack && tv > -1.0 && tv < qmaxd + 1.0 && nok && m0 + R + jj < M) push_fix(R + jj, cl, 0);
           });
           if (MODE == 1) return;
           if (g.out16) {
@@ -468,7 +476,84 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const int cnt = fix_cnt;
   if (cnt == 0) return;
   const bool full = cnt > kFixCap;  // list overflowed: recompute the whole tile exactly
-  const int total = full ? rows_real * cols_real : cnt;
+  int total = full ? rows_real * cols_real : cnt;
+  if (!A16 && !full) {
+    // 8-bit activations, exact in integers.  With s32 = M * 2^E the oracle's weight is
+    // fl32(w * s32) = 2^E * (w * M + r) for an integer residue r, so the exact dot product is
+    // 2^E * D with D = M * (acc + corr) + sum_k (a_k - 128) r_k + (128 - zp) * sum_k r_k.
+    // All 256 threads form the residue sum Y = sum_k (a_k - 128) r_k of a batch of listed
+    // outputs at once (one K chunk of 16 per thread per output), reduced with integer LDS
+    // atomics (order-independent).  Only outputs whose exact value is still within the oracle's
+    // own float64 noise of a rounding boundary are handed to the float64 emulation below.
+    int *ysum = reinterpret_cast<int *>(arena);                  // [kFixCap]
+    uint32_t *unc = reinterpret_cast<uint32_t *>(arena) + kFixCap;  // [kFixCap]
+    for (int e = t; e < cnt; e += kGemmThreads) ysum[e] = 0;
+    __syncthreads();
+    constexpr int EB = 4;  // listed outputs whose loads are in flight together
+    const int KC = K / 16;
+    for (int e0 = 0; e0 < cnt; e0 += EB) {
+      // the loop bound is uniform so that every lane of a wave takes part in the reduction
+      for (int kc0 = 0; kc0 < KC; kc0 += kGemmThreads) {
+        const bool kin = kc0 + t < KC;
+        const int k = kin ? (kc0 + t) * 16 : 0;
+        int w[EB][16];
+        uint4 av[EB];
+        int nloc[EB];
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {
+          const int e = e0 + i < cnt ? e0 + i : cnt - 1;
+          const uint32_t v = fix_list[e];
+          const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
+          nloc[i] = n;
+          load_w16<TFMT, LPBQ>(g, n, k, w[i]);
+          av[i] = *reinterpret_cast<const uint4 *>(act + static_cast<size_t>(m) * K + k);
+        }
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {
+          const int n = nloc[i];
+          const float sc = g.s32[n];
+          const double ip = g.inv_pow2e[n];
+          const int mant = static_cast<int>(g.mant[n]);
+          int y = 0;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int a = static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i])[j]) - 128;
+            const float wd = static_cast<float>(w[i][j]) * sc;
+            const int wp = static_cast<int>(static_cast<double>(wd) * ip);  // exact integer
+            y += a * (wp - w[i][j] * mant);
+          }
+          if (!kin) y = 0;
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) y += __shfl_xor(y, off, 64);
+          if (lane == 0 && e0 + i < cnt) atomicAdd(&ysum[e0 + i], y);
+        }
+      }
+    }
+    __syncthreads();
+    for (int e = t; e < cnt; e += kGemmThreads) {
+      const uint32_t v = fix_list[e];
+      const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
+      const int64_t D = g.mant[n] * (static_cast<int64_t>(fix_acc[e]) + g.corr[n]) + ysum[e] +
+                        static_cast<int64_t>(128 - g.act_zp) * g.colsum_r[n];
+      const double u = static_cast<double>(D) * g.alpha_e[n];
+      const double tv = u + g.beta[n];
+      const double rd = rint(tv);
+      const double slack = g.margin_exact[n] + 0x1p-48 * (fabs(u) + fabs(tv) + g.absb[n]);
+      if (fabs(tv - rd) > 0.5 - slack) {
+        unc[atomicAdd(&unc_cnt, 1)] = v;
+      } else {
+        const int oi = static_cast<int>(rd);
+        store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
+      }
+    }
+    __syncthreads();
+    total = unc_cnt;
+    for (int e = wave; e < total; e += kGemmThreads / 64) {
+      const uint32_t v = unc[e];
+      fixup_one<A16, TFMT, LPBQ>(g, m0 + static_cast<int>(v >> 16), n0 + static_cast<int>(v & 0xFFFFu), lane);
+    }
+    return;
+  }
   for (int e = wave; e < total; e += kGemmThreads / 64) {
     int r, c;
     if (full) {
@@ -511,6 +596,10 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.corr = D.corr;
   g.mant = D.mant;
   g.colsum = D.colsum;
+  g.colsum_r = D.colsum_r;
+  g.alpha_e = D.alpha_e;
+  g.inv_pow2e = D.inv_pow2e;
+  g.margin_exact = D.margin_exact;
   g.s32 = D.s32;
   g.M = m;
   g.N = sh.N;

@@ -274,7 +274,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   std::vector<double> alpha(Np, 0.0), beta(Np, 0.0), margin(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0), mr1(Np, 0.0);
   std::vector<int64_t> corr(Np, 0), mantv(Np, 0), csum(Np, 0), csum_r(Np, 0);
   std::vector<double> alpha_e(Np, 0.0);
-  std::vector<int32_t> expov(Np, 0);
+  std::vector<double> inv_pow2e(Np, 1.0), margin_exact(Np, 0.0);
   std::vector<float> s32v(Np, 1.0f);
   const double a_base = a16 ? 32768.0 : 128.0;  // the kernels shift activations by this
   for (int n = 0; n < N; ++n) {
@@ -302,7 +302,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     csum[n] = colsum_q[n];
     csum_r[n] = colsum_r[n];
     alpha_e[n] = sA * two_e / sO;
-    expov[n] = expo[n];
+    inv_pow2e[n] = std::ldexp(1.0, -expo[n]);
+    margin_exact[n] = inv_sO * sA * two_e * noise * kSafety;
     s32v[n] = s;
   }
 
@@ -331,7 +332,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.colsum, csum);
   if (st == QH_STATUS_OK) st = al.upload(&D.colsum_r, csum_r);
   if (st == QH_STATUS_OK) st = al.upload(&D.alpha_e, alpha_e);
-  if (st == QH_STATUS_OK) st = al.upload(&D.expo, expov);
+  if (st == QH_STATUS_OK) st = al.upload(&D.inv_pow2e, inv_pow2e);
+  if (st == QH_STATUS_OK) st = al.upload(&D.margin_exact, margin_exact);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
   if (st != QH_STATUS_OK) {
     al.release();

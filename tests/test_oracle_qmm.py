@@ -156,3 +156,17 @@ def test_w4a16_lpbq_native_zero_point():
     w = np.ones((64, 8), np.int64)
     act = np.full((1, 64), 32768, np.uint16)
     np.testing.assert_array_equal(qmm.w4a16_lpbq_scalar_native(act, w), 32768)
+
+
+@pytest.mark.parametrize("fam", ["u8i8", "w4a8_per_channel", "w4a8_lpbq"])
+def test_near_tie_stress_covers_both_fixup_regimes(fam):
+    """The near-tie GPU case must flag a few hundred outputs in row tile 0 (per-tile list) and
+    more than the list capacity (1024) in row tile 1 (whole-tile recomputation)."""
+    from stress_cases import flagged_per_tile, near_tie_case, stress_layout
+
+    m, k, n, tie, zero, rail = stress_layout()
+    c = near_tie_case(fam, m, k, n, 5, tie, zero, rail)
+    d = qmm.dequantized_output(c.activation_q, qmm._w_int(c), c.weight_scale, c.bias_q, c.act_scale, c.family.act_zp)
+    f = flagged_per_tile(c, d)
+    assert 100 < f[0, 0] < 1024, f
+    assert f[1, 0] > 1024, f

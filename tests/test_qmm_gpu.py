@@ -137,3 +137,20 @@ def test_invalid_arguments_report_status(gpu):
     with pytest.raises(_lib.QhtpError):
         op(torch.zeros((32, 128), dtype=torch.uint8, device=gpu), path=2)  # M=32 > 16 on the GEMV
     op.close()
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+def test_near_tie_outputs_bit_exact(gpu, fam):
+    """Outputs packed next to rounding boundaries: per-tile lists under and over capacity
+    (8-bit activations), exact ties left to the float64 emulation, ragged column tile."""
+    from stress_cases import near_tie_case, stress_layout
+
+    m, k, n, tie, zero, rail = stress_layout()
+    c = near_tie_case(fam, m, k, n, 5, tie, zero, rail)
+    want = oq.expected_output_case(c)
+    print(f"[qmm] {fam} near-tie {m}x{k}x{n} gemm", flush=True)
+    got = run(c, gpu, path=1)
+    assert np.array_equal(got, want), f"gemm: {diff_msg(got, want)}"
+    print(f"[qmm] {fam} near-tie rows 0..15 gemv", flush=True)
+    got = run(c, gpu, path=2, rows=16)
+    assert np.array_equal(got, want[:16]), f"gemv: {diff_msg(got, want[:16])}"
