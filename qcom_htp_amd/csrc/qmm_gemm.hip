@@ -53,7 +53,8 @@ struct GemmArgs {
   const uint8_t *tiles;
   const uint8_t *lpbq;
   const double *alpha, *beta, *margin, *absb, *bias_deq;
-  const double *alpha_e, *inv_pow2e, *margin_exact;
+  const double *alpha_e, *margin_exact;
+  const int32_t *scale_exp;
   const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
   int M, N, K, KT, TM, TN;
@@ -126,6 +127,87 @@ __device__ __forceinline__ void load_w16(const GemmArgs g, int cb, int k, int (&
   }
 }
 
+// Lane q of a quad holds outputs o[0..3] of tile rows R..R+3 in its own column; the quad
+// exchanges them (DPP quad broadcasts + byte permutes) so that lane q stores tile row
+// row = R + q, tile columns col..col+3 (4 adjacent outputs in one store).
+__device__ __forceinline__ void store_strip(const GemmArgs &g, uint8_t *tile_out, int m0, int n0, int row, int col,
+                                            const int (&o)[4], int q, bool full) {
+  const bool ok = full || (m0 + row < g.M && n0 + col < g.N);
+  const uint32_t off = static_cast<uint32_t>(row) * static_cast<uint32_t>(g.N) + static_cast<uint32_t>(col);
+  if (!g.out16) {
+    const uint32_t p = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 8) |
+                       (static_cast<uint32_t>(o[2]) << 16) | (static_cast<uint32_t>(o[3]) << 24);
+    const uint32_t x0 = __builtin_amdgcn_mov_dpp(p, 0x00, 0xF, 0xF, false);
+    const uint32_t x1 = __builtin_amdgcn_mov_dpp(p, 0x55, 0xF, 0xF, false);
+    const uint32_t x2 = __builtin_amdgcn_mov_dpp(p, 0xAA, 0xF, 0xF, false);
+    const uint32_t x3 = __builtin_amdgcn_mov_dpp(p, 0xFF, 0xF, 0xF, false);
+    const uint32_t sel = static_cast<uint32_t>(q) | (static_cast<uint32_t>(4 + q) << 8) | 0x0C0C0000u;
+    const uint32_t w = perm(perm(x3, x2, sel), perm(x1, x0, sel), 0x05040100u);
+    if (ok) *reinterpret_cast<uint32_t *>(tile_out + off) = w;
+  } else {
+    const uint32_t P0 = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
+    const uint32_t P1 = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
+    // every lane fetches both strips of every quad lane, then keeps the half it stores (a
+    // lane-dependent choice between DPP results must come after all DPPs)
+    const uint32_t a0 = __builtin_amdgcn_mov_dpp(P0, 0x00, 0xF, 0xF, false);
+    const uint32_t a1 = __builtin_amdgcn_mov_dpp(P0, 0x55, 0xF, 0xF, false);
+    const uint32_t a2 = __builtin_amdgcn_mov_dpp(P0, 0xAA, 0xF, 0xF, false);
+    const uint32_t a3 = __builtin_amdgcn_mov_dpp(P0, 0xFF, 0xF, 0xF, false);
+    const uint32_t b0 = __builtin_amdgcn_mov_dpp(P1, 0x00, 0xF, 0xF, false);
+    const uint32_t b1 = __builtin_amdgcn_mov_dpp(P1, 0x55, 0xF, 0xF, false);
+    const uint32_t b2 = __builtin_amdgcn_mov_dpp(P1, 0xAA, 0xF, 0xF, false);
+    const uint32_t b3 = __builtin_amdgcn_mov_dpp(P1, 0xFF, 0xF, 0xF, false);
+    const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
+    const uint32_t lo_w = perm(a1, a0, sel), hi_w = perm(a3, a2, sel);
+    const uint32_t lo_w2 = perm(b1, b0, sel), hi_w2 = perm(b3, b2, sel);
+    const uint2 w = q < 2 ? make_uint2(lo_w, hi_w) : make_uint2(lo_w2, hi_w2);
+    if (ok) *reinterpret_cast<uint2 *>(tile_out + 2 * off) = w;
+  }
+}
+
+__device__ __forceinline__ int clamp_out(int v, int qmax) { return min(max(v, 0), qmax); }
+
+// rint(t) without the float64 round / convert instructions: adding 1.5 * 2^52 leaves the
+// rounded integer (ties to even) in the low word, exact for |t| < 2^31.  CLAMP first limits t
+// to [-1, qmax + 1] (used when |t| < 2^30 is not proven for every column); rint then lands
+// on -1 or qmax + 1 for t outside, whose output is 0 or qmax whichever way t rounds.
+// Returns |t - rint(t)|.
+template <bool CLAMP>
+__device__ __forceinline__ double round_near(double t, double qmax, int *oi) {
+  constexpr double kMagic = 6755399441055744.0;  // 1.5 * 2^52
+  const double tc = CLAMP ? fmin(fmax(t, -1.0), qmax + 1.0) : t;
+  const double y = tc + kMagic;
+  *oi = __double2loint(y);
+  return fabs(tc - (y - kMagic));
+}
+
+// 16 consecutive weights of operand column cb, kept packed: I8 codes in v, or int4 nibbles in
+// v.x / v.y (byte j: k = j low nibble, k = j + 8 high nibble) with the LPBQ block scale f.
+struct WRaw {
+  uint4 v;
+  int f;
+};
+template <int TFMT, bool LPBQ>
+__device__ __forceinline__ WRaw load_w16_raw(const GemmArgs &g, int cb, int k) {
+  const size_t tile = static_cast<size_t>(cb / kBN) * g.KT + k / kBK;
+  WRaw r;
+  r.f = 1;
+  if (TFMT == kTileI8) {
+    r.v = *reinterpret_cast<const uint4 *>(g.tiles + tile * (kBN * kBK) + tile_off_i8(cb % kBN, k));
+  } else {
+    const uint2 h = *reinterpret_cast<const uint2 *>(g.tiles + tile * (kBN * kBK / 2) + tile_off_i4(cb % kBN, k));
+    r.v = make_uint4(h.x, h.y, 0u, 0u);
+    if (LPBQ) r.f = g.lpbq[tile * (kBN * 4) + (cb % kBN) * 4 + ((k & 127) >> 5)];
+  }
+  return r;
+}
+template <int TFMT>
+__device__ __forceinline__ int w_at(const WRaw &r, int j) {
+  if (TFMT == kTileI8) return reinterpret_cast<const int8_t *>(&r.v)[j];
+  const int b = reinterpret_cast<const uint8_t *>(&r.v)[j & 7];
+  return ((j < 8 ? (b & 15) : (b >> 4)) - 8) * r.f;
+}
+
 // Exact float64 recomputation of one output, term by term as the oracle forms it:
 // sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), then + bias_deq, / sO, + out_zp, rint, clip.
 template <bool A16, int TFMT, bool LPBQ>
@@ -196,13 +278,17 @@ __device__ __forceinline__ void tile_of(int w, int TM, int TN, int *tm, int *tn)
 }
 
 // MODE 0: requantised output; MODE 1: exact int64 accumulators sum_k (a - zp) * w_int.
-template <bool A16, int TFMT, bool LPBQ, int MODE>
+// CLAMP: clamp t before rounding (some column cannot prove |t| < 2^30).
+template <bool A16, int TFMT, bool LPBQ, int MODE, bool CLAMP>
 __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArgs g) {
   using C = Cfg<A16, TFMT, LPBQ>;
   __shared__ __attribute__((aligned(16))) uint8_t arena[C::kArena];
-  __shared__ uint32_t fix_list[kFixCap];
-  __shared__ int fix_acc[A16 ? 1 : kFixCap];  // 8-bit acts: int32 accumulator of each listed output
-  __shared__ int fix_cnt, unc_cnt;
+  __shared__ uint32_t fix_list[kFixCap];  // (row << 16 | column) inside the tile
+  __shared__ int fix_cnt;
+  // Per-column epilogue constants of the tile, filled while the first operand tiles load.
+  //   8-bit acts : [alpha | beta' | thr] x 256 columns;
+  //   16-bit acts: [alpha | alpha * M | beta' | thr] x 128 columns.
+  __shared__ double ctab[MODE == 0 ? 768 : 1];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -216,10 +302,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const uint8_t *const act = g.act;
   const uint8_t *const btiles = g.tiles + static_cast<size_t>(tn) * KT * C::kTileB;
   const uint8_t *const ftiles = LPBQ ? g.lpbq + static_cast<size_t>(tn) * KT * C::kTileF : nullptr;
-  if (t == 0) {
-    fix_cnt = 0;
-    unc_cnt = 0;
-  }
+  if (t == 0) fix_cnt = 0;
 
   auto stage_a = [&](int st) { return arena + st * C::kStageBytes; };
   auto stage_b = [&](int st) { return arena + st * C::kStageBytes + kTileA; };
@@ -260,10 +343,44 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   v16i acc[4][4];
   static_for<4>([&](auto i) { static_for<4>([&](auto j) { acc[i][j] = v16i{}; }); });
 
+  // Per-column constants: loads issued ahead of the operand prologue, LDS writes after it (so
+  // only these loads are waited for).
+  double cv[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
+  int64_t ccorr = 0, cmant = 0;
+  const int ccol = A16 ? (t & 127) : t;
+  const int cn = n0 + ccol < g.N ? n0 + ccol : 0;
+  if (MODE == 0) {
+    cv[0] = g.alpha[cn];
+    cv[1] = g.beta[cn];
+    cv[2] = g.margin[cn];
+    cv[3] = g.absb[cn];
+    ccorr = g.corr[cn];
+    if (A16) cmant = g.mant[cn];
+  }
   constexpr int S = C::kStages;
 #pragma unroll
   for (int p = 0; p < S - 1; ++p)
     if (p < KT) issue(p, p);
+  if (MODE == 0) {
+    const double alpha = cv[0];
+    // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
+    const double betap = fma(static_cast<double>(ccorr), alpha, cv[1]);
+    const double corr_term = 2.0 * fabs(static_cast<double>(ccorr) * alpha);
+    if (!A16) {
+      // |t - rint(t)| <= thr certifies the rounding; slack for |t| <= qmax + 2 folded in
+      ctab[t] = alpha;
+      ctab[256 + t] = betap;
+      ctab[512 + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + static_cast<double>(g.out_qmax) + 2.0);
+    } else if (t < 128) {
+      // t = Y * alpha + (X * alpha M + beta'); |X| <= K * 33024 * 127 bounds the float slack
+      const double alpha_m = alpha * static_cast<double>(cmant);
+      const double umax = fabs(alpha_m) * static_cast<double>(K) * (33024.0 * 127.0);
+      ctab[t] = alpha;
+      ctab[128 + t] = alpha_m;
+      ctab[256 + t] = betap;
+      ctab[384 + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + umax + static_cast<double>(g.out_qmax) + 2.0);
+    }
+  }
 
   const int g32 = lane >> 5;  // which 16-k half of a 32-k MFMA step this lane supplies
   for (int kt = 0; kt < KT; ++kt) {
@@ -332,248 +449,273 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     }
   }
   // ---------------------------------------------------------------- epilogue
-  // Straight from the accumulator registers: each lane requantises the 4 rows x 1 column
-  // strips of its MFMA blocks, then the 4 lanes of a quad transpose their strips (DPP quad
+  // Straight from the accumulator registers: each lane requantises the 4-row strips of its
+  // MFMA blocks (one column), then the 4 lanes of a quad transpose their strips (DPP quad
   // broadcasts + byte permutes) so every lane stores 4 adjacent outputs of one row.
-  auto push_fix = [&](int r, int c, int a) {
-    const int slot = atomicAdd(&fix_cnt, 1);
-    if (slot < kFixCap) {
-      fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(c);
-      if (!A16) fix_acc[slot] = a;
-    }
-  };
+  // Rounding: t + 1.5 * 2^52 leaves rint(t) in the low word (|t| < 2^30 is proven per
+  // column at prepare time, otherwise t is clamped first).  A strip whose largest
+  // |t - rint(t)| exceeds the column's certified threshold takes a rare path that marks its
+  // uncertain outputs in LDS (in the operand arena every wave has finished reading; the marks
+  // must not stay in registers).  Marks: one dword per thread and 32x32 block, byte jg = strip
+  // jg, bit jj = row jj.  A mark is needed only if rint(t) lies in [0, qmax] (otherwise both
+  // candidate roundings clamp to the same output).
   const int q = lane & 3;
   const double qmaxd = static_cast<double>(g.out_qmax);
+  constexpr int kBlocks = A16 ? 4 : 16;  // 32-row x 32-column blocks per lane
+  uint32_t *const flagw = reinterpret_cast<uint32_t *>(arena);  // [kBlocks][256 threads]
+  uint8_t *const flagb = arena;
+  if (MODE == 1) {
+    // exact int64 accumulators sum_k (a - zp) * w_int
+    if (!A16) {
+      static_for<4>([&](auto nt) {
+        const int n = n0 + wn * 128 + nt * 32 + (lane & 31);
+        if (n >= g.N) return;
+        const int64_t corr = g.corr[n];
+        static_for<4>([&](auto mt) {
+          static_for<16>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const int m = m0 + wm * 128 + mt * 32 + 8 * (j / 4) + 4 * (lane >> 5) + (j % 4);
+            if (m < M)
+              reinterpret_cast<int64_t *>(g.out)[static_cast<size_t>(m) * g.N + n] = static_cast<int64_t>(acc[mt][nt][j]) + corr;
+          });
+        });
+      });
+    } else {
+      static_for<2>([&](auto c) {
+        const int n = n0 + wn * 64 + c * 32 + (lane & 31);
+        if (n >= g.N) return;
+        const int64_t csum = g.colsum[n] * static_cast<int64_t>(128 + 32768 - g.act_zp);
+        static_for<2>([&](auto mt) {
+          static_for<16>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const int m = m0 + wm * 64 + mt * 32 + 8 * (j / 4) + 4 * (lane >> 5) + (j % 4);
+            if (m < M)
+              reinterpret_cast<int64_t *>(g.out)[static_cast<size_t>(m) * g.N + n] =
+                  256 * static_cast<int64_t>(acc[2 * mt][2 * c][j]) + acc[2 * mt + 1][2 * c][j] + csum;
+          });
+        });
+      });
+    }
+    return;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < kBlocks; ++b) flagw[b * kGemmThreads + t] = 0u;  // this thread's own marks
+  const int esz = g.out16 ? 2 : 1;
+  uint8_t *const tile_out = static_cast<uint8_t *>(g.out) + (static_cast<size_t>(m0) * g.N + n0) * esz;
+  const bool full = m0 + rows_real <= M && n0 + cols_real <= g.N;
   if (!A16) {
     static_for<4>([&](auto nt) {
       const int cl = wn * 128 + nt * 32 + (lane & 31);  // column inside the tile
-      const int n = n0 + cl;
-      const bool nok = n < g.N;
-      const int nn = nok ? n : 0;
-      double alpha, beta, thr;
-      if (MODE == 0) {
-        alpha = g.alpha[nn];
-        // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
-        beta = fma(static_cast<double>(g.corr[nn]), alpha, g.beta[nn]);
-        // |t - rint(t)| <= thr certifies the rounding; slack for |t| <= qmax + 2 folded in
-        thr = 0.5 - g.margin[nn] - 0x1p-48 * (g.absb[nn] + 2.0 * fabs(g.corr[nn] * alpha) + qmaxd + 2.0);
-      }
+      const double alpha = ctab[cl], beta = ctab[256 + cl], thr = ctab[512 + cl];
       static_for<4>([&](auto mt) {
         static_for<4>([&](auto jg) {
           const int R = wm * 128 + mt * 32 + 8 * jg + 4 * (lane >> 5);  // first of 4 rows
           int o[4];
+          double dmax = 0.0;
           static_for<4>([&](auto jj) {
-            constexpr int j = 4 * decltype(jg)::value + decltype(jj)::value;
-            const int a = acc[mt][nt][j];
-            if (MODE == 1) {
-              if (nok && m0 + R + jj < M)
-                reinterpret_cast<int64_t *>(g.out)[static_cast<size_t>(m0 + R + jj) * g.N + n] =
-                    static_cast<int64_t>(a) + g.corr[nn];
-              return;
-            }
-            const double tv = fma(static_cast<double>(a), alpha, beta);
-            const double rd = rint(tv);
-            int oi = static_cast<int>(rd);
-            o[jj] = oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi);
-            if (fabs(tv - rd) > thr && tv > -1.0 && tv < qmaxd + 1.0 && nok && m0 + R + jj < M) push_fix(R + jj, cl, a);
+            const double tv = fma(static_cast<double>(acc[mt][nt][4 * decltype(jg)::value + decltype(jj)::value]), alpha, beta);
+            int oi;
+            dmax = fmax(dmax, round_near<CLAMP>(tv, qmaxd, &oi));
+            o[jj] = clamp_out(oi, g.out_qmax);
           });
-          if (MODE == 1) return;
-          if (!g.out16) {
-            const uint32_t p = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 8) |
-                               (static_cast<uint32_t>(o[2]) << 16) | (static_cast<uint32_t>(o[3]) << 24);
-            const uint32_t x0 = __builtin_amdgcn_mov_dpp(p, 0x00, 0xF, 0xF, false);
-            const uint32_t x1 = __builtin_amdgcn_mov_dpp(p, 0x55, 0xF, 0xF, false);
-            const uint32_t x2 = __builtin_amdgcn_mov_dpp(p, 0xAA, 0xF, 0xF, false);
-            const uint32_t x3 = __builtin_amdgcn_mov_dpp(p, 0xFF, 0xF, 0xF, false);
-            const uint32_t sel = static_cast<uint32_t>(q) | (static_cast<uint32_t>(4 + q) << 8) | 0x0C0C0000u;
-            const uint32_t w = perm(perm(x3, x2, sel), perm(x1, x0, sel), 0x05040100u);
-            const int row = m0 + R + q, col = n0 + wn * 128 + nt * 32 + (lane & 28);
-            if (row < M && col < g.N) *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(g.out) + static_cast<size_t>(row) * g.N + col) = w;
-          } else {
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-              if (nok && m0 + R + jj < M) store_out(g.out, 1, static_cast<size_t>(m0 + R + jj) * g.N + n, o[jj]);
+          if (dmax > thr) {  // rare: mark the uncertain outputs of the strip
+            uint32_t fm = 0;
+            static_for<4>([&](auto jj) {
+              const double tv = fma(static_cast<double>(acc[mt][nt][4 * decltype(jg)::value + decltype(jj)::value]), alpha, beta);
+              int oi;
+              const double d = round_near<CLAMP>(tv, qmaxd, &oi);
+              fm |= static_cast<uint32_t>((d > thr) & (static_cast<uint32_t>(oi) <= static_cast<uint32_t>(g.out_qmax))) << jj;
+            });
+            flagb[((nt * 4 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(fm);
           }
+          store_strip(g, tile_out, m0, n0, R + q, wn * 128 + nt * 32 + (lane & 28), o, q, full);
         });
       });
     });
   } else {
     // 16-bit activations: real row tiles mt (32 rows), real column tiles c (32 columns);
     // acc[2mt + p][2c + s]: p = hi / lo' activation byte, s = weight code / rounding residue.
+    // X = sum (a-32768)' q and Y = sum (a-32768)' r are exact in float64.
     static_for<2>([&](auto c) {
       const int cl = wn * 64 + c * 32 + (lane & 31);
-      const int n = n0 + cl;
-      const bool nok = n < g.N;
-      const int nn = nok ? n : 0;
-      double alpha = 0, alpha_m = 0, beta = 0, margin = 0, absb = 0;
-      const int64_t csum = MODE == 1 ? g.colsum[nn] * static_cast<int64_t>(128 + 32768 - g.act_zp) : 0;
-      if (MODE == 0) {
-        alpha = g.alpha[nn];
-        alpha_m = alpha * static_cast<double>(g.mant[nn]);
-        beta = fma(static_cast<double>(g.corr[nn]), alpha, g.beta[nn]);
-        margin = g.margin[nn];
-        absb = g.absb[nn] + 2.0 * fabs(static_cast<double>(g.corr[nn]) * alpha);
-      }
+      const double alpha = ctab[cl], alpha_m = ctab[128 + cl], beta = ctab[256 + cl], thr = ctab[384 + cl];
       static_for<2>([&](auto mt) {
         static_for<4>([&](auto jg) {
           const int R = wm * 64 + mt * 32 + 8 * jg + 4 * (lane >> 5);
-          int o[4];
-          static_for<4>([&](auto jj) {
+          auto t_of = [&](auto jj) {
             constexpr int j = 4 * decltype(jg)::value + decltype(jj)::value;
-            const int hq = acc[2 * mt][2 * c][j], lq = acc[2 * mt + 1][2 * c][j];
-            const int hr = acc[2 * mt][2 * c + 1][j], lr = acc[2 * mt + 1][2 * c + 1][j];
-            if (MODE == 1) {
-              if (nok && m0 + R + jj < M)
-                reinterpret_cast<int64_t *>(g.out)[static_cast<size_t>(m0 + R + jj) * g.N + n] =
-                    256 * static_cast<int64_t>(hq) + lq + csum;
-              return;
-            }
-            // exact: X = sum (a-32768)' q, Y = sum (a-32768)' r as float64 integers
-            const double X = fma(static_cast<double>(hq), 256.0, static_cast<double>(lq));
-            const double Y = fma(static_cast<double>(hr), 256.0, static_cast<double>(lr));
-            const double u = X * alpha_m;
-            const double tv = fma(Y, alpha, u + beta);
-            const double rd = rint(tv);
-            int oi = static_cast<int>(rd);
-            o[jj] = oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi);
-            const double slack = margin + 0x1p-48 * (fabs(u) + fabs(tv) + absb);
-            if (fabs(tv - rd) > 0.5 - slack && tv > -1.0 && tv < qmaxd + 1.0 && nok && m0 + R + jj < M) push_fix(R + jj, cl, 0);
+            const double X = fma(static_cast<double>(acc[2 * mt][2 * c][j]), 256.0, static_cast<double>(acc[2 * mt + 1][2 * c][j]));
+            const double Y = fma(static_cast<double>(acc[2 * mt][2 * c + 1][j]), 256.0, static_cast<double>(acc[2 * mt + 1][2 * c + 1][j]));
+            return fma(Y, alpha, fma(X, alpha_m, beta));
+          };
+          int o[4];
+          double dmax = 0.0;
+          static_for<4>([&](auto jj) {
+            int oi;
+            dmax = fmax(dmax, round_near<CLAMP>(t_of(jj), qmaxd, &oi));
+            o[jj] = clamp_out(oi, g.out_qmax);
           });
-          if (MODE == 1) return;
-          if (g.out16) {
-            const uint32_t P0 = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
-            const uint32_t P1 = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
-            // every lane fetches both strips of every quad lane, then keeps the half it stores
-            const uint32_t a0 = __builtin_amdgcn_mov_dpp(P0, 0x00, 0xF, 0xF, false);
-            const uint32_t a1 = __builtin_amdgcn_mov_dpp(P0, 0x55, 0xF, 0xF, false);
-            const uint32_t a2 = __builtin_amdgcn_mov_dpp(P0, 0xAA, 0xF, 0xF, false);
-            const uint32_t a3 = __builtin_amdgcn_mov_dpp(P0, 0xFF, 0xF, 0xF, false);
-            const uint32_t b0 = __builtin_amdgcn_mov_dpp(P1, 0x00, 0xF, 0xF, false);
-            const uint32_t b1 = __builtin_amdgcn_mov_dpp(P1, 0x55, 0xF, 0xF, false);
-            const uint32_t b2 = __builtin_amdgcn_mov_dpp(P1, 0xAA, 0xF, 0xF, false);
-            const uint32_t b3 = __builtin_amdgcn_mov_dpp(P1, 0xFF, 0xF, 0xF, false);
-            const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
-            const uint32_t lo_w = perm(a1, a0, sel), hi_w = perm(a3, a2, sel);
-            const uint32_t lo_w2 = perm(b1, b0, sel), hi_w2 = perm(b3, b2, sel);
-            const uint2 w = q < 2 ? make_uint2(lo_w, hi_w) : make_uint2(lo_w2, hi_w2);
-            const int row = m0 + R + q, col = n0 + wn * 64 + c * 32 + (lane & 28);
-            if (row < M && col < g.N)
-              *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(g.out) + static_cast<size_t>(row) * g.N + col) = w;
-          } else {
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-              if (nok && m0 + R + jj < M) store_out(g.out, 0, static_cast<size_t>(m0 + R + jj) * g.N + n, o[jj]);
+          if (dmax > thr) {  // rare: mark the uncertain outputs of the strip
+            uint32_t fm = 0;
+            static_for<4>([&](auto jj) {
+              int oi;
+              const double d = round_near<CLAMP>(t_of(jj), qmaxd, &oi);
+              fm |= static_cast<uint32_t>((d > thr) & (static_cast<uint32_t>(oi) <= static_cast<uint32_t>(g.out_qmax))) << jj;
+            });
+            flagb[((c * 2 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(fm);
           }
+          store_strip(g, tile_out, m0, n0, R + q, wn * 64 + c * 32 + (lane & 28), o, q, full);
         });
       });
     });
   }
-  if (MODE == 1) return;
-  __syncthreads();  // provisional outputs of flagged elements are stored before the fixup rewrites them
-
 
   // ---------------------------------------------------------------- exact fixup
-  const int cnt = fix_cnt;
-  if (cnt == 0) return;
-  const bool full = cnt > kFixCap;  // list overflowed: recompute the whole tile exactly
-  int total = full ? rows_real * cols_real : cnt;
-  if (!A16 && !full) {
-    // 8-bit activations, exact in integers.  With s32 = M * 2^E the oracle's weight is
-    // fl32(w * s32) = 2^E * (w * M + r) for an integer residue r, so the exact dot product is
-    // 2^E * D with D = M * (acc + corr) + sum_k (a_k - 128) r_k + (128 - zp) * sum_k r_k.
-    // All 256 threads form the residue sum Y = sum_k (a_k - 128) r_k of a batch of listed
-    // outputs at once (one K chunk of 16 per thread per output), reduced with integer LDS
-    // atomics (order-independent).  Only outputs whose exact value is still within the oracle's
-    // own float64 noise of a rounding boundary are handed to the float64 emulation below.
-    int *ysum = reinterpret_cast<int *>(arena);                  // [kFixCap]
-    uint32_t *unc = reinterpret_cast<uint32_t *>(arena) + kFixCap;  // [kFixCap]
-    for (int e = t; e < cnt; e += kGemmThreads) ysum[e] = 0;
+  // With s32 = M * 2^E the oracle's weight is fl32(w * s32) = 2^E * W', W' = w * M + r for an
+  // integer residue r, so the exact dot product is 2^E * D with
+  //   D = sum_k (a_k - zp) W'_k = M * S1 + S2 + (base - zp) * (M * sum_k w_k + sum_k r_k),
+  //   S1 = sum_k (a_k - base) w_k,  S2 = sum_k (a_k - base) r_k   (base = 128 or 32768).
+  // Marked outputs are listed in passes of at most kFixCap.  Each wave takes whole outputs
+  // (EW at a time, P 16-deep K chunks per lane in flight), forms S1 and S2 exactly in integers
+  // and decides: t = D * sA * 2^E / sO + beta rounds like the oracle unless t is still within
+  // the oracle's own float64 noise of a boundary; those outputs get the float64 emulation of
+  // the oracle's dot product.
+  const int abase = A16 ? 32768 : 128;
+  const int KC = K / 16;
+  constexpr int P = 4;   // K chunks per lane in flight per output
+  constexpr int EW = 2;  // outputs per wave in flight together
+  for (;;) {
+    __syncthreads();  // marks complete; provisional outputs stored before any rewrite
+    uint32_t marks[kBlocks];
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) marks[b] = flagw[b * kGemmThreads + t];
+#pragma unroll
+    for (int b = 0; b < kBlocks; ++b) {
+      uint32_t mk = marks[b];
+      if (mk == 0) continue;
+      uint32_t keep = 0;
+      const int rb = A16 ? wm * 64 + (b & 1) * 32 + 4 * (lane >> 5) : wm * 128 + (b & 3) * 32 + 4 * (lane >> 5);
+      const int c = A16 ? wn * 64 + (b >> 1) * 32 + (lane & 31) : wn * 128 + (b >> 2) * 32 + (lane & 31);
+      while (mk) {
+        const int bit = __builtin_ctz(mk);
+        mk &= mk - 1;
+        const int r = rb + 8 * (bit >> 3) + (bit & 7);
+        if (m0 + r >= M || n0 + c >= g.N) continue;  // padding rows / columns of the tile
+        const int slot = atomicAdd(&fix_cnt, 1);
+        if (slot < kFixCap)
+          fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(c);
+        else
+          keep |= 1u << bit;  // listed in a later pass
+      }
+      flagw[b * kGemmThreads + t] = keep;
+    }
     __syncthreads();
-    constexpr int EB = 4;  // listed outputs whose loads are in flight together
-    const int KC = K / 16;
-    for (int e0 = 0; e0 < cnt; e0 += EB) {
-      // the loop bound is uniform so that every lane of a wave takes part in the reduction
-      for (int kc0 = 0; kc0 < KC; kc0 += kGemmThreads) {
-        const bool kin = kc0 + t < KC;
-        const int k = kin ? (kc0 + t) * 16 : 0;
-        int w[EB][16];
-        uint4 av[EB];
-        int nloc[EB];
+    const int total = fix_cnt;
+    if (total == 0) break;
+    const int cnt = total < kFixCap ? total : kFixCap;
+    for (int e0 = wave * EW; e0 < cnt; e0 += (kGemmThreads / 64) * EW) {
+      // every per-output constant is requested together with the first operand chunks
+      int mrow[EW], ncol[EW], sexp[EW], mant[EW];
+      float sc[EW];
+      int64_t csq[EW], csr[EW];
+      double ae[EW], bt[EW], mx[EW], ab[EW];
 #pragma unroll
-        for (int i = 0; i < EB; ++i) {
-          const int e = e0 + i < cnt ? e0 + i : cnt - 1;
-          const uint32_t v = fix_list[e];
-          const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
-          nloc[i] = n;
-          load_w16<TFMT, LPBQ>(g, n, k, w[i]);
-          av[i] = *reinterpret_cast<const uint4 *>(act + static_cast<size_t>(m) * K + k);
-        }
+      for (int i = 0; i < EW; ++i) {
+        const int e = e0 + i < cnt ? e0 + i : cnt - 1;
+        const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);  // uniform in the wave
+        mrow[i] = m0 + static_cast<int>(v >> 16);
+        const int n = n0 + static_cast<int>(v & 0xFFFFu);
+        ncol[i] = n;
+        sc[i] = g.s32[n];
+        sexp[i] = g.scale_exp[n];
+        mant[i] = static_cast<int>(g.mant[n]);
+        csq[i] = g.colsum[n];
+        csr[i] = g.colsum_r[n];
+        ae[i] = g.alpha_e[n];
+        bt[i] = g.beta[n];
+        mx[i] = g.margin_exact[n];
+        ab[i] = g.absb[n];
+      }
+      long long S1[EW], S2[EW];
 #pragma unroll
-        for (int i = 0; i < EB; ++i) {
-          const int n = nloc[i];
-          const float sc = g.s32[n];
-          const double ip = g.inv_pow2e[n];
-          const int mant = static_cast<int>(g.mant[n]);
-          int y = 0;
+      for (int i = 0; i < EW; ++i) S1[i] = S2[i] = 0;
+      for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
+        WRaw wr[EW][P];
+        uint4 av[EW][P][A16 ? 2 : 1];
 #pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int a = static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i])[j]) - 128;
-            const float wd = static_cast<float>(w[i][j]) * sc;
-            const int wp = static_cast<int>(static_cast<double>(wd) * ip);  // exact integer
-            y += a * (wp - w[i][j] * mant);
+        for (int i = 0; i < EW; ++i) {
+#pragma unroll
+          for (int pp = 0; pp < P; ++pp) {
+            const int kc = kc0 + lane + 64 * pp;
+            const int k = kc < KC ? kc * 16 : 0;
+            const int n = ncol[i];
+            wr[i][pp] = load_w16_raw<TFMT, LPBQ>(g, A16 ? (n / 32) * 64 + (n % 32) : n, k);
+            const uint4 *ap = reinterpret_cast<const uint4 *>(act + (static_cast<size_t>(mrow[i]) * K + k) * (A16 ? 2 : 1));
+            av[i][pp][0] = ap[0];
+            if (A16) av[i][pp][A16 ? 1 : 0] = ap[1];
           }
-          if (!kin) y = 0;
+        }
 #pragma unroll
-          for (int off = 32; off >= 1; off >>= 1) y += __shfl_xor(y, off, 64);
-          if (lane == 0 && e0 + i < cnt) atomicAdd(&ysum[e0 + i], y);
+        for (int i = 0; i < EW; ++i) {
+          int s1 = 0, s2 = 0;  // |.| < 2^28 for P * 16 terms
+#pragma unroll
+          for (int pp = 0; pp < P; ++pp) {
+            if (kc0 + lane + 64 * pp >= KC) continue;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int a = (A16 ? static_cast<int>(reinterpret_cast<const uint16_t *>(&av[i][pp][j >> 3])[j & 7])
+                                 : static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i][pp][0])[j])) - abase;
+              const int wj = w_at<TFMT>(wr[i][pp], j);
+              // W' = fl32(w * s32) / 2^E, an integer below 2^31: exact in float32 and int32
+              const int wp = static_cast<int>(ldexpf(static_cast<float>(wj) * sc[i], -sexp[i]));
+              s1 += a * wj;
+              s2 += a * (wp - wj * mant[i]);
+            }
+          }
+          S1[i] += s1;
+          S2[i] += s2;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < EW; ++i) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          S1[i] += __shfl_xor(S1[i], off, 64);
+          S2[i] += __shfl_xor(S2[i], off, 64);
+        }
+        if (e0 + i >= cnt) continue;
+        const int m = mrow[i], n = ncol[i];
+        // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
+        const unsigned long long M64 = static_cast<unsigned long long>(static_cast<long long>(mant[i]));
+        const unsigned long long sw = M64 * static_cast<unsigned long long>(csq[i]) + static_cast<unsigned long long>(csr[i]);
+        const unsigned long long Du = M64 * static_cast<unsigned long long>(S1[i]) + static_cast<unsigned long long>(S2[i]) +
+                                      static_cast<unsigned long long>(static_cast<long long>(abase - g.act_zp)) * sw;
+        const double u = static_cast<double>(static_cast<long long>(Du)) * ae[i];
+        const double tv = u + bt[i];
+        const double rd = rint(tv);
+        const double slack = mx[i] + 0x1p-48 * (fabs(u) + fabs(tv) + ab[i]);
+        if (fabs(tv - rd) > 0.5 - slack) {
+          fixup_one<A16, TFMT, LPBQ>(g, m, n, lane);
+        } else if (lane == 0) {
+          const int oi = static_cast<int>(rd);
+          store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
         }
       }
     }
+    if (total <= kFixCap) break;
     __syncthreads();
-    for (int e = t; e < cnt; e += kGemmThreads) {
-      const uint32_t v = fix_list[e];
-      const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
-      const int64_t D = g.mant[n] * (static_cast<int64_t>(fix_acc[e]) + g.corr[n]) + ysum[e] +
-                        static_cast<int64_t>(128 - g.act_zp) * g.colsum_r[n];
-      const double u = static_cast<double>(D) * g.alpha_e[n];
-      const double tv = u + g.beta[n];
-      const double rd = rint(tv);
-      const double slack = g.margin_exact[n] + 0x1p-48 * (fabs(u) + fabs(tv) + g.absb[n]);
-      if (fabs(tv - rd) > 0.5 - slack) {
-        unc[atomicAdd(&unc_cnt, 1)] = v;
-      } else {
-        const int oi = static_cast<int>(rd);
-        store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
-      }
-    }
-    __syncthreads();
-    total = unc_cnt;
-    for (int e = wave; e < total; e += kGemmThreads / 64) {
-      const uint32_t v = unc[e];
-      fixup_one<A16, TFMT, LPBQ>(g, m0 + static_cast<int>(v >> 16), n0 + static_cast<int>(v & 0xFFFFu), lane);
-    }
-    return;
-  }
-  for (int e = wave; e < total; e += kGemmThreads / 64) {
-    int r, c;
-    if (full) {
-      r = e / cols_real;
-      c = e % cols_real;
-    } else {
-      const uint32_t v = fix_list[e];
-      r = static_cast<int>(v >> 16);
-      c = static_cast<int>(v & 0xFFFFu);
-    }
-    const int m = m0 + r, n = n0 + c;
-    if (m >= M || n >= g.N) continue;
-    fixup_one<A16, TFMT, LPBQ>(g, m, n, lane);
+    if (t == 0) fix_cnt = 0;
   }
 }
 
 template <bool A16, int TFMT, bool LPBQ, int MODE>
-qh_status launch(const GemmArgs &g, hipStream_t stream) {
+qh_status launch(const GemmArgs &g, bool clamp, hipStream_t stream) {
   dim3 grid(g.TM * g.TN);
-  hipLaunchKernelGGL((qmm_gemm_kernel<A16, TFMT, LPBQ, MODE>), grid, dim3(kGemmThreads), 0, stream, g);
+  if (MODE == 0 && clamp)
+    hipLaunchKernelGGL((qmm_gemm_kernel<A16, TFMT, LPBQ, MODE, true>), grid, dim3(kGemmThreads), 0, stream, g);
+  else
+    hipLaunchKernelGGL((qmm_gemm_kernel<A16, TFMT, LPBQ, MODE, false>), grid, dim3(kGemmThreads), 0, stream, g);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "qmm_gemm_kernel launch");
   return QH_STATUS_OK;
@@ -598,7 +740,7 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.colsum = D.colsum;
   g.colsum_r = D.colsum_r;
   g.alpha_e = D.alpha_e;
-  g.inv_pow2e = D.inv_pow2e;
+  g.scale_exp = D.scale_exp;
   g.margin_exact = D.margin_exact;
   g.s32 = D.s32;
   g.M = m;
@@ -617,13 +759,14 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.TM = (m + rows_real - 1) / rows_real;
   if (static_cast<long long>(g.TM) * g.TN > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "M=%d too large", m);
   const bool lpbq_regs = sh.wfmt == QH_WEIGHT_I4_LPBQ && !a16;
+  const bool clamp = sh.epi_clamp != 0;
   if (!a16) {
-    if (sh.tile_fmt == kTileI8) return launch<false, kTileI8, false, MODE>(g, stream);
-    if (lpbq_regs) return launch<false, kTileI4, true, MODE>(g, stream);
-    return launch<false, kTileI4, false, MODE>(g, stream);
+    if (sh.tile_fmt == kTileI8) return launch<false, kTileI8, false, MODE>(g, clamp, stream);
+    if (lpbq_regs) return launch<false, kTileI4, true, MODE>(g, clamp, stream);
+    return launch<false, kTileI4, false, MODE>(g, clamp, stream);
   }
-  if (sh.tile_fmt == kTileI8) return launch<true, kTileI8, false, MODE>(g, stream);
-  return launch<true, kTileI4, false, MODE>(g, stream);
+  if (sh.tile_fmt == kTileI8) return launch<true, kTileI8, false, MODE>(g, clamp, stream);
+  return launch<true, kTileI4, false, MODE>(g, clamp, stream);
 }
 
 }  // namespace

@@ -65,7 +65,7 @@ struct QmmDevice {
   int64_t *colsum;  // sum_k w_int[n][k]
   int64_t *colsum_r; // sum_k r[n][k] (float32 rounding residues of the dequantised weights)
   double *alpha_e;  // sA * 2^E / sO: output LSB per unit of the exact integer dot product in 2^E units
-  double *inv_pow2e; // 2^-E of s32 = M * 2^E
+  int32_t *scale_exp; // E of s32 = M * 2^E
   double *margin_exact; // 8-bit acts: float64 noise bound of the oracle's dot product, output LSB
   double *gemv_margin_r1; // 16-bit acts GEMV: per-channel coefficient of R1[m] in the margin
 };
@@ -82,6 +82,7 @@ struct QmmShape {
   int lpbq_block;     // 0 unless LPBQ
   int act_zp, out_zp;
   double act_scale, out_scale;
+  int epi_clamp;      // GEMM epilogue must clamp t before rounding (|t| < 2^30 not proven)
 };
 
 }  // namespace qh

@@ -274,7 +274,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   std::vector<double> alpha(Np, 0.0), beta(Np, 0.0), margin(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0), mr1(Np, 0.0);
   std::vector<int64_t> corr(Np, 0), mantv(Np, 0), csum(Np, 0), csum_r(Np, 0);
   std::vector<double> alpha_e(Np, 0.0);
-  std::vector<double> inv_pow2e(Np, 1.0), margin_exact(Np, 0.0);
+  std::vector<double> margin_exact(Np, 0.0);
+  std::vector<int32_t> scale_exp(Np, 0);
   std::vector<float> s32v(Np, 1.0f);
   const double a_base = a16 ? 32768.0 : 128.0;  // the kernels shift activations by this
   for (int n = 0; n < N; ++n) {
@@ -297,12 +298,20 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
       mr1[n] = inv_sO * sA * two_e * rmax[n] * kSafety;  // GEMV: residue term bound per unit R1
     }
     beta[n] = bdeq[n] / sO + d->out_zp;
+    {
+      // Largest |t| the GEMM epilogue can see for this column (t = acc * alpha + beta'); the
+      // epilogue's rounding shortcut needs |t| < 2^31, otherwise t is clamped first.
+      const double betap = std::fabs(beta[n]) + std::fabs(static_cast<double>(corr[n]) * alpha[n]);
+      const double tmax = a16 ? (std::fabs(alpha[n]) * static_cast<double>(mant[n]) + std::fabs(alpha[n])) * K * 33024.0 * 127.0 + betap
+                              : std::fabs(alpha[n]) * K * 128.0 * 127.0 + betap;
+      if (!(tmax < 1073741824.0)) sh.epi_clamp = 1;
+    }
     absb[n] = 2.0 * std::fabs(beta[n]) + 2.0 * d->out_zp + 1.0;
     mantv[n] = mant[n];
     csum[n] = colsum_q[n];
     csum_r[n] = colsum_r[n];
     alpha_e[n] = sA * two_e / sO;
-    inv_pow2e[n] = std::ldexp(1.0, -expo[n]);
+    scale_exp[n] = expo[n];
     margin_exact[n] = inv_sO * sA * two_e * noise * kSafety;
     s32v[n] = s;
   }
@@ -332,7 +341,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.colsum, csum);
   if (st == QH_STATUS_OK) st = al.upload(&D.colsum_r, csum_r);
   if (st == QH_STATUS_OK) st = al.upload(&D.alpha_e, alpha_e);
-  if (st == QH_STATUS_OK) st = al.upload(&D.inv_pow2e, inv_pow2e);
+  if (st == QH_STATUS_OK) st = al.upload(&D.scale_exp, scale_exp);
   if (st == QH_STATUS_OK) st = al.upload(&D.margin_exact, margin_exact);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
   if (st != QH_STATUS_OK) {
