@@ -277,12 +277,180 @@ __device__ __forceinline__ void tile_of(int w, int TM, int TN, int *tm, int *tn)
   *tn = in / gm;
 }
 
+// ---------------------------------------------------------------- main loop pieces
+// Everything the k loop needs about the workgroup's tile.
+struct MainCtx {
+  const uint8_t *act;     // activations [M][K] (u8) or [M][K] (u16)
+  const uint8_t *btiles;  // weight tiles of this column panel, one per 128-k step
+  const uint8_t *ftiles;  // LPBQ block-scale tiles of this column panel
+  int M, K, m0, t, lane, wave, wm, wn;
+};
+
+// Issue the direct-to-LDS loads of k-tile kt into the stage (wa, wb, wf).
+template <bool A16, int TFMT, bool LPBQ>
+__device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__restrict__ wa, uint8_t *__restrict__ wb,
+                                           uint8_t *__restrict__ wf) {
+  using C = Cfg<A16, TFMT, LPBQ>;
+#pragma unroll
+  for (int j = 0; j < C::kLoadsA; ++j) {
+    const int slot = j * 256 + c.t;  // 16-byte slot of the tile
+    const void *src;
+    if (!A16) {
+      const int row = slot >> 3, phys = slot & 7;
+      const int logical = phys ^ swz8(row);
+      const int m = c.m0 + row < c.M ? c.m0 + row : c.M - 1;
+      const int k = kt * kBK + 16 * logical < c.K ? kt * kBK + 16 * logical : c.K - 16;
+      src = c.act + static_cast<size_t>(m) * c.K + k;
+    } else {
+      const int row = slot >> 4, phys = slot & 15;
+      const int logical = phys ^ swz16(row);
+      const int m = c.m0 + row < c.M ? c.m0 + row : c.M - 1;
+      const int k = kt * kBK + 8 * logical < c.K ? kt * kBK + 8 * logical : c.K - 8;
+      src = c.act + (static_cast<size_t>(m) * c.K + k) * 2;
+    }
+    load_lds16(src, wa + (j * 256 + c.wave * 64) * 16);
+  }
+  const uint8_t *bsrc = c.btiles + static_cast<size_t>(kt) * C::kTileB;
+#pragma unroll
+  for (int j = 0; j < C::kLoadsB; ++j) load_lds16(bsrc + (j * 256 + c.t) * 16, wb + (j * 256 + c.wave * 64) * 16);
+  if (LPBQ) {
+    const uint8_t *fsrc = c.ftiles + static_cast<size_t>(kt) * C::kTileF;
+    if (c.lane < 16) load_lds16(fsrc + (c.wave * 16 + c.lane) * 16, wf + c.wave * 256);
+  }
+}
+
+// Raw LDS words of one 32-k step: A fragments and B fragments (int4 tiles use .x/.y).
+struct RawStep {
+  uint4 a[4];
+  uint4 b[4];
+};
+
+template <bool A16, int TFMT>
+__device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__restrict__ la, const uint8_t *__restrict__ lb,
+                                          int kk, RawStep &r) {
+  const int s16 = 2 * kk + (c.lane >> 5);  // 16-k chunk index inside the 128-k tile
+  if (!A16) {
+    static_for<4>([&](auto mt) {
+      const int row = c.wm * 128 + mt * 32 + (c.lane & 31);
+      r.a[mt] = *reinterpret_cast<const uint4 *>(la + row * 128 + 16 * (s16 ^ swz8(row)));
+    });
+  } else {
+    static_for<2>([&](auto mt) {
+      const int row = c.wm * 64 + mt * 32 + (c.lane & 31);
+      r.a[2 * mt] = *reinterpret_cast<const uint4 *>(la + row * 256 + 16 * ((2 * s16) ^ swz16(row)));
+      r.a[2 * mt + 1] = *reinterpret_cast<const uint4 *>(la + row * 256 + 16 * ((2 * s16 + 1) ^ swz16(row)));
+    });
+  }
+  static_for<4>([&](auto nt) {
+    const int col = c.wn * 128 + nt * 32 + (c.lane & 31);
+    if (TFMT == kTileI8) {
+      r.b[nt] = *reinterpret_cast<const uint4 *>(lb + col * 128 + 16 * (s16 ^ swz8(col)));
+    } else {
+      // the offset is hidden from the compiler so that it does not merge the four 8-byte reads
+      // into ds_read2 pairs (the merged reads lose the no-alias information and would wait
+      // for the loads in flight)
+      int off = col * 64 + 8 * (s16 ^ swz_i4(col));
+      asm volatile("" : "+v"(off));
+      const uint2 v = *reinterpret_cast<const uint2 *>(lb + off);
+      r.b[nt] = make_uint4(v.x, v.y, 0u, 0u);
+    }
+  });
+}
+
+// Raw words -> MFMA operands: activations to signed bytes (16-bit: hi / lo' byte planes),
+// int4 weights widened (with the LPBQ block scale of the step).
+template <bool A16, int TFMT, bool LPBQ>
+__device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&fcol)[4], int kk, v4i (&af)[4], v4i (&bf)[4]) {
+  if (!A16) {
+    static_for<4>([&](auto mt) {
+      const uint4 v = r.a[mt];
+      af[mt] = v4i{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
+                   static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
+    });
+  } else {
+    static_for<2>([&](auto mt) {
+      uint4 v0 = r.a[2 * mt], v1 = r.a[2 * mt + 1];
+      v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
+      v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
+      af[2 * mt] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x07050301u)), static_cast<int>(perm(v0.w, v0.z, 0x07050301u)),
+                       static_cast<int>(perm(v1.y, v1.x, 0x07050301u)), static_cast<int>(perm(v1.w, v1.z, 0x07050301u))};
+      af[2 * mt + 1] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x06040200u)), static_cast<int>(perm(v0.w, v0.z, 0x06040200u)),
+                           static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
+    });
+  }
+  static_for<4>([&](auto nt) {
+    const uint4 v = r.b[nt];
+    if (TFMT == kTileI8) {
+      bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
+    } else {
+      uint32_t f = 1;
+      if (LPBQ) f = (fcol[nt] >> (8 * kk)) & 0xFFu;
+      const uint32_t bias = (128u - 8u * f) * 0x01010101u;
+      const uint32_t m4 = 0x0F0F0F0Fu;
+      bf[nt] = v4i{static_cast<int>(widen4(v.x & m4, f, bias)), static_cast<int>(widen4(v.y & m4, f, bias)),
+                   static_cast<int>(widen4((v.x >> 4) & m4, f, bias)), static_cast<int>(widen4((v.y >> 4) & m4, f, bias))};
+    }
+  });
+}
+
+// One 128-k step on the tile held in (la, lb, lf), after issuing the loads of tile
+// kt + S - 1 into (wa, wb, wf).  The read and written stages are distinct LDS objects passed
+// as restrict pointers: the compiler may then let fragment reads run while the loads are in
+// flight (it would otherwise wait for every load before each read).  Fragment reads of the
+// next 32-k step are issued before the MFMAs of the current one.
+template <bool A16, int TFMT, bool LPBQ>
+__device__ __forceinline__ void k_step(const MainCtx &c, int kt, int KT, const uint8_t *__restrict__ la,
+                                       const uint8_t *__restrict__ lb, const uint8_t *__restrict__ lf,
+                                       uint8_t *__restrict__ wa, uint8_t *__restrict__ wb, uint8_t *__restrict__ wf,
+                                       v16i (&acc)[4][4]) {
+  using C = Cfg<A16, TFMT, LPBQ>;
+  constexpr int S = C::kStages;
+  // tile kt has landed once at most (S-2) later tiles are still in flight
+  if (S == 3 && kt + 1 < KT)
+    wait_vmcnt<(S - 2) * C::kLoads>();
+  else
+    wait_vmcnt<0>();
+  // Workgroup barrier without the release fence of __syncthreads: that fence would wait for
+  // every load in flight.  Each wave has waited for its own loads of tile kt above, and all of
+  // its reads of the stage refilled next were consumed before it arrives here.
+  asm volatile("s_barrier" ::: "memory");
+  uint32_t fcol[4] = {1u, 1u, 1u, 1u};
+  if (LPBQ) {
+    static_for<4>([&](auto nt) {
+      const int col = c.wn * 128 + nt * 32 + (c.lane & 31);
+      fcol[nt] = *reinterpret_cast<const uint32_t *>(lf + col * 4);
+    });
+  }
+  RawStep raw[2];
+  v4i af[4], bf[4];
+  read_step<A16, TFMT>(c, la, lb, 0, raw[0]);
+  if (kt + S - 1 < KT) issue_tile<A16, TFMT, LPBQ>(c, kt + S - 1, wa, wb, wf);
+  convert_step<A16, TFMT, LPBQ>(raw[0], fcol, 0, af, bf);
+  static_for<4>([&](auto kkc) {
+    constexpr int kk = decltype(kkc)::value;
+    if (kk < 3) read_step<A16, TFMT>(c, la, lb, kk + 1, raw[(kk + 1) & 1]);
+    static_for<4>([&](auto mt) {
+      static_for<4>([&](auto nt) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
+      });
+    });
+    if (kk < 3) convert_step<A16, TFMT, LPBQ>(raw[(kk + 1) & 1], fcol, kk + 1, af, bf);
+  });
+}
+
 // MODE 0: requantised output; MODE 1: exact int64 accumulators sum_k (a - zp) * w_int.
 // CLAMP: clamp t before rounding (some column cannot prove |t| < 2^30).
 template <bool A16, int TFMT, bool LPBQ, int MODE, bool CLAMP>
 __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArgs g) {
   using C = Cfg<A16, TFMT, LPBQ>;
-  __shared__ __attribute__((aligned(16))) uint8_t arena[C::kArena];
+  // One LDS object per pipeline stage and operand: the compiler then knows that the
+  // direct-to-LDS loads in flight (into other stages) cannot alias the fragment reads, and
+  // does not make the reads wait for them.
+  constexpr int S = C::kStages;
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kTileA], sA1[kTileA], sA2[S > 2 ? kTileA : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sB0[C::kTileB], sB1[C::kTileB], sB2[S > 2 ? C::kTileB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sF0[LPBQ ? C::kTileF : 16], sF1[LPBQ ? C::kTileF : 16],
+      sF2[LPBQ && S > 2 ? C::kTileF : 16];
   __shared__ uint32_t fix_list[kFixCap];  // (row << 16 | column) inside the tile
   __shared__ int fix_cnt;
   // Per-column epilogue constants of the tile, filled while the first operand tiles load.
@@ -304,41 +472,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const uint8_t *const ftiles = LPBQ ? g.lpbq + static_cast<size_t>(tn) * KT * C::kTileF : nullptr;
   if (t == 0) fix_cnt = 0;
 
-  auto stage_a = [&](int st) { return arena + st * C::kStageBytes; };
-  auto stage_b = [&](int st) { return arena + st * C::kStageBytes + kTileA; };
-  auto stage_f = [&](int st) { return arena + st * C::kStageBytes + kTileA + C::kTileB; };
+  // stage indices are compile-time constants everywhere (the k loop is unrolled by S)
+  auto stage_a = [&](auto st) -> uint8_t * { return st == 0 ? sA0 : (st == 1 ? sA1 : sA2); };
+  auto stage_b = [&](auto st) -> uint8_t * { return st == 0 ? sB0 : (st == 1 ? sB1 : sB2); };
+  auto stage_f = [&](auto st) -> uint8_t * { return st == 0 ? sF0 : (st == 1 ? sF1 : sF2); };
 
-  // Issue the direct-to-LDS loads of k-tile kt into stage st (kLoads instructions per wave).
-  auto issue = [&](int kt, int st) {
-    uint8_t *la = stage_a(st);
-#pragma unroll
-    for (int j = 0; j < C::kLoadsA; ++j) {
-      const int slot = j * 256 + t;  // 16-byte slot of the tile
-      const void *src;
-      if (!A16) {
-        const int row = slot >> 3, phys = slot & 7;
-        const int logical = phys ^ swz8(row);
-        const int m = m0 + row < M ? m0 + row : M - 1;
-        const int k = kt * kBK + 16 * logical < K ? kt * kBK + 16 * logical : K - 16;
-        src = act + static_cast<size_t>(m) * K + k;
-      } else {
-        const int row = slot >> 4, phys = slot & 15;
-        const int logical = phys ^ swz16(row);
-        const int m = m0 + row < M ? m0 + row : M - 1;
-        const int k = kt * kBK + 8 * logical < K ? kt * kBK + 8 * logical : K - 8;
-        src = act + (static_cast<size_t>(m) * K + k) * 2;
-      }
-      load_lds16(src, la + (j * 256 + wave * 64) * 16);
-    }
-    const uint8_t *bsrc = btiles + static_cast<size_t>(kt) * C::kTileB;
-    uint8_t *lb = stage_b(st);
-#pragma unroll
-    for (int j = 0; j < C::kLoadsB; ++j) load_lds16(bsrc + (j * 256 + t) * 16, lb + (j * 256 + wave * 64) * 16);
-    if (LPBQ) {
-      const uint8_t *fsrc = ftiles + static_cast<size_t>(kt) * C::kTileF;
-      if (lane < 16) load_lds16(fsrc + (wave * 16 + lane) * 16, stage_f(st) + wave * 256);
-    }
-  };
+  const MainCtx mc{act, btiles, ftiles, M, K, m0, t, lane, wave, wm, wn};
 
   v16i acc[4][4];
   static_for<4>([&](auto i) { static_for<4>([&](auto j) { acc[i][j] = v16i{}; }); });
@@ -357,10 +496,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     ccorr = g.corr[cn];
     if (A16) cmant = g.mant[cn];
   }
-  constexpr int S = C::kStages;
-#pragma unroll
-  for (int p = 0; p < S - 1; ++p)
-    if (p < KT) issue(p, p);
+  static_for<S - 1>([&](auto p) {
+    if (p < KT) issue_tile<A16, TFMT, LPBQ>(mc, p, stage_a(p), stage_b(p), stage_f(p));
+  });
   if (MODE == 0) {
     const double alpha = cv[0];
     // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
@@ -382,72 +520,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     }
   }
 
-  const int g32 = lane >> 5;  // which 16-k half of a 32-k MFMA step this lane supplies
-  for (int kt = 0; kt < KT; ++kt) {
-    // tile kt has landed once at most (S-2) later tiles are still in flight
-    if (S == 3 && kt + 1 < KT)
-      wait_vmcnt<(S - 2) * C::kLoads>();
-    else
-      wait_vmcnt<0>();
-    __syncthreads();
-    if (kt + S - 1 < KT) issue(kt + S - 1, (kt + S - 1) % S);
-    const int st = kt % S;
-    const uint8_t *la = stage_a(st);
-    const uint8_t *lb = stage_b(st);
-    uint32_t fcol[4];
-    if (LPBQ) {
-      static_for<4>([&](auto nt) {
-        const int col = wn * 128 + nt * 32 + (lane & 31);
-        fcol[nt] = *reinterpret_cast<const uint32_t *>(stage_f(st) + col * 4);
-      });
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int s16 = 2 * kk + g32;  // 16-k chunk index inside the 128-k tile
-      v4i af[4], bf[4];
-      if (!A16) {
-        static_for<4>([&](auto mt) {
-          const int row = wm * 128 + mt * 32 + (lane & 31);
-          uint4 v = *reinterpret_cast<const uint4 *>(la + row * 128 + 16 * (s16 ^ swz8(row)));
-          af[mt] = v4i{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
-                       static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
-        });
-      } else {
-        static_for<2>([&](auto mt) {
-          const int row = wm * 64 + mt * 32 + (lane & 31);
-          uint4 v0 = *reinterpret_cast<const uint4 *>(la + row * 256 + 16 * ((2 * s16) ^ swz16(row)));
-          uint4 v1 = *reinterpret_cast<const uint4 *>(la + row * 256 + 16 * ((2 * s16 + 1) ^ swz16(row)));
-          v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
-          v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
-          af[2 * mt] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x07050301u)), static_cast<int>(perm(v0.w, v0.z, 0x07050301u)),
-                           static_cast<int>(perm(v1.y, v1.x, 0x07050301u)), static_cast<int>(perm(v1.w, v1.z, 0x07050301u))};
-          af[2 * mt + 1] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x06040200u)), static_cast<int>(perm(v0.w, v0.z, 0x06040200u)),
-                               static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
-        });
-      }
-      static_for<4>([&](auto nt) {
-        const int col = wn * 128 + nt * 32 + (lane & 31);
-        if (TFMT == kTileI8) {
-          const uint4 v = *reinterpret_cast<const uint4 *>(lb + col * 128 + 16 * (s16 ^ swz8(col)));
-          bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-        } else {
-          const uint2 v = *reinterpret_cast<const uint2 *>(lb + col * 64 + 8 * (s16 ^ swz_i4(col)));
-          uint32_t f = 1;
-          if (LPBQ) f = (fcol[nt] >> (8 * kk)) & 0xFFu;
-          const uint32_t bias = (128u - 8u * f) * 0x01010101u;
-          const uint32_t m4 = 0x0F0F0F0Fu;
-          bf[nt] = v4i{static_cast<int>(widen4(v.x & m4, f, bias)), static_cast<int>(widen4(v.y & m4, f, bias)),
-                       static_cast<int>(widen4((v.x >> 4) & m4, f, bias)),
-                       static_cast<int>(widen4((v.y >> 4) & m4, f, bias))};
-        }
-      });
-      static_for<4>([&](auto mt) {
-        static_for<4>([&](auto nt) {
-          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
-        });
-      });
-    }
-  }
+  // k loop, unrolled by the stage count so every stage is a compile-time LDS object
+  auto step = [&](const int kt, auto sc) __attribute__((always_inline)) {
+    constexpr int rs = decltype(sc)::value, ws = (rs + S - 1) % S;
+    k_step<A16, TFMT, LPBQ>(mc, kt, KT, stage_a(rs), stage_b(rs), stage_f(rs), stage_a(ws), stage_b(ws), stage_f(ws), acc);
+  };
+  int kt0 = 0;
+  for (; kt0 + S <= KT; kt0 += S) static_for<S>([&](auto sc) { step(kt0 + sc, sc); });
+  static_for<S - 1>([&](auto sc) {
+    if (kt0 + sc < KT) step(kt0 + sc, sc);
+  });
   // ---------------------------------------------------------------- epilogue
   // Straight from the accumulator registers: each lane requantises the 4-row strips of its
   // MFMA blocks (one column), then the 4 lanes of a quad transpose their strips (DPP quad
@@ -455,15 +537,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // Rounding: t + 1.5 * 2^52 leaves rint(t) in the low word (|t| < 2^30 is proven per
   // column at prepare time, otherwise t is clamped first).  A strip whose largest
   // |t - rint(t)| exceeds the column's certified threshold takes a rare path that marks its
-  // uncertain outputs in LDS (in the operand arena every wave has finished reading; the marks
+  // uncertain outputs in LDS (in an operand stage every wave has finished reading; the marks
   // must not stay in registers).  Marks: one dword per thread and 32x32 block, byte jg = strip
   // jg, bit jj = row jj.  A mark is needed only if rint(t) lies in [0, qmax] (otherwise both
   // candidate roundings clamp to the same output).
   const int q = lane & 3;
   const double qmaxd = static_cast<double>(g.out_qmax);
   constexpr int kBlocks = A16 ? 4 : 16;  // 32-row x 32-column blocks per lane
-  uint32_t *const flagw = reinterpret_cast<uint32_t *>(arena);  // [kBlocks][256 threads]
-  uint8_t *const flagb = arena;
+  uint32_t *const flagw = reinterpret_cast<uint32_t *>(sA0);  // [kBlocks][256 threads]
+  uint8_t *const flagb = sA0;
   if (MODE == 1) {
     // exact int64 accumulators sum_k (a - zp) * w_int
     if (!A16) {
