@@ -211,7 +211,7 @@ __device__ __forceinline__ int w_at(const WRaw &r, int j) {
 // Exact float64 recomputation of one output, term by term as the oracle forms it:
 // sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), then + bias_deq, / sO, + out_zp, rint, clip.
 template <bool A16, int TFMT, bool LPBQ>
-__device__ __noinline__ void fixup_one(const GemmArgs g, int m, int n, int lane) {
+__device__ __forceinline__ void fixup_one(const GemmArgs &g, int m, int n, int lane) {
   const int cb = A16 ? (n / 32) * 64 + (n % 32) : n;
   const float sc = g.s32[n];
   double s = 0.0;
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const int abase = A16 ? 32768 : 128;
   const int KC = K / 16;
   constexpr int P = 4;   // K chunks per lane in flight per output
-  constexpr int EW = 2;  // outputs per wave in flight together
+  constexpr int EW = 1;  // outputs per wave in flight together
   for (;;) {
     __syncthreads();  // marks complete; provisional outputs stored before any rewrite
     uint32_t marks[kBlocks];
@@ -698,8 +698,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     const int cnt = total < kFixCap ? total : kFixCap;
     for (int e0 = wave * EW; e0 < cnt; e0 += (kGemmThreads / 64) * EW) {
       // every per-output constant is requested together with the first operand chunks
-      int mrow[EW], ncol[EW], sexp[EW], mant[EW];
-      float sc[EW];
+      int mrow[EW], ncol[EW], mant[EW];
+      float mf[EW];
       int64_t csq[EW], csr[EW];
       double ae[EW], bt[EW], mx[EW], ab[EW];
 #pragma unroll
@@ -709,9 +709,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
         mrow[i] = m0 + static_cast<int>(v >> 16);
         const int n = n0 + static_cast<int>(v & 0xFFFFu);
         ncol[i] = n;
-        sc[i] = g.s32[n];
-        sexp[i] = g.scale_exp[n];
         mant[i] = static_cast<int>(g.mant[n]);
+        mf[i] = static_cast<float>(mant[i]);  // exact: M < 2^24
         csq[i] = g.colsum[n];
         csr[i] = g.colsum_r[n];
         ae[i] = g.alpha_e[n];
@@ -749,10 +748,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
               const int a = (A16 ? static_cast<int>(reinterpret_cast<const uint16_t *>(&av[i][pp][j >> 3])[j & 7])
                                  : static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i][pp][0])[j])) - abase;
               const int wj = w_at<TFMT>(wr[i][pp], j);
-              // W' = fl32(w * s32) / 2^E, an integer below 2^31: exact in float32 and int32
-              const int wp = static_cast<int>(ldexpf(static_cast<float>(wj) * sc[i], -sexp[i]));
-              s1 += a * wj;
-              s2 += a * (wp - wj * mant[i]);
+              // W' = fl32(w * s32) / 2^E = fl32(w * M) (s32 = M * 2^E, no subnormals): the
+              // residue r = W' - w * M is minus the exact rounding error of that product
+              const float wf = static_cast<float>(wj);
+              const float prod = __fmul_rn(wf, mf[i]);
+              const int r = -static_cast<int>(__fmaf_rn(wf, mf[i], -prod));
+              s1 += __mul24(a, wj);
+              s2 += __mul24(a, r);
             }
           }
           S1[i] += s1;
