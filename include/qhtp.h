@@ -152,6 +152,25 @@ qh_status qh_gdn_solve_f32(const float *A_dev, float *T_dev, uint32_t heads, uin
 qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t heads, uint32_t C, int32_t zpA,
                            int32_t zpT, float sA, float sT, uint32_t precision, void *stream);
 
+
+/* Fused GDN chunk products (the intra-chunk half of the gated delta rule,
+ * scripts/gdn_ref_kernel.py:71-89).  For every batch b, chunk c of `chunk` tokens and head h:
+ *   K^ = l2norm(K) (eps 1e-6), g = cumsum of the per-token log decay gc inside the chunk,
+ *   A_ij = -beta_i (K^_i . K^_j) e^{g_i - g_j} for i > j,  T = (I - A)^-1,
+ *   U = T (beta * V),  W = T (beta * K^)   [W = T (beta * K^ * e^g) with QH_GDN_W_DECAY].
+ * k_dev, v_dev: bf16 bit patterns [batch][tokens][heads][head_dim]; g_dev (gc) and beta_dev:
+ * float32 [batch][tokens][heads]; w_dev, u_dev: [batch][tokens][heads][head_dim], bf16 bit
+ * patterns, or float32 with QH_GDN_OUT_F32.  head_dim == 128, chunk in {64, 128, 256},
+ * tokens % chunk == 0.  bf16 MFMA with fp32 accumulation (tolerance: the bf16 bound, 1.05e-2
+ * relative Frobenius against float64).  Buffers must be 16-byte aligned. */
+enum {
+  QH_GDN_W_DECAY = 1u, /* W = T (beta * K^ * e^g) (the reference kernel's form)           */
+  QH_GDN_OUT_F32 = 2u, /* W and U as float32 instead of bf16                             */
+};
+qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
+                          void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
+                          uint32_t head_dim, uint32_t chunk, uint32_t flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

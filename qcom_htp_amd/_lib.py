@@ -25,6 +25,9 @@ QH_WEIGHT_I4_LPBQ = 2
 QH_GDN_FP32 = 0
 QH_GDN_BF16 = 1
 
+QH_GDN_W_DECAY = 1
+QH_GDN_OUT_F32 = 2
+
 # Every symbol include/qhtp.h declares (checked by the CPU test-suite).
 EXPORTED = (
     "qh_status_string",
@@ -38,6 +41,7 @@ EXPORTED = (
     "qh_qmm_release",
     "qh_gdn_solve_f32",
     "qh_gdn_solve_u16",
+    "qh_gdn_chunk_uw",
 )
 
 
@@ -114,6 +118,8 @@ def _declare(L: C.CDLL) -> None:
     L.qh_gdn_solve_f32.restype = st
     L.qh_gdn_solve_u16.argtypes = [vp, vp, u32, u32, i32, i32, f32, f32, u32, vp]
     L.qh_gdn_solve_u16.restype = st
+    L.qh_gdn_chunk_uw.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp]
+    L.qh_gdn_chunk_uw.restype = st
 
 
 def lib() -> C.CDLL:

@@ -146,4 +146,28 @@ qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t head
                               static_cast<int>(precision), static_cast<hipStream_t>(stream));
 }
 
+
+qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
+                          void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
+                          uint32_t head_dim, uint32_t chunk, uint32_t flags, void *stream) {
+  if (!k_dev || !v_dev || !g_dev || !beta_dev || !w_dev || !u_dev)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_uw: NULL buffer");
+  if (head_dim != 128) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: head_dim=%u (need 128)", head_dim);
+  if (chunk != 64 && chunk != 128 && chunk != 256)
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: chunk=%u (need 64, 128 or 256)", chunk);
+  if (batch == 0 || heads == 0 || tokens == 0 || tokens % chunk)
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: batch=%u tokens=%u heads=%u (tokens %% chunk == 0)",
+                batch, tokens, heads);
+  if (static_cast<uint64_t>(batch) * tokens * heads > (1ull << 31) / 128)
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: batch * tokens * heads too large");
+  if (flags & ~static_cast<uint32_t>(QH_GDN_W_DECAY | QH_GDN_OUT_F32))
+    return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_chunk_uw: unknown flags 0x%x", flags);
+  const uintptr_t al = reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev) |
+                       reinterpret_cast<uintptr_t>(w_dev) | reinterpret_cast<uintptr_t>(u_dev);
+  if (al % 16) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_uw: k, v, w, u must be 16-byte aligned");
+  return launch_gdn_chunk_uw(k_dev, v_dev, g_dev, beta_dev, w_dev, u_dev, static_cast<int>(batch),
+                             static_cast<int>(tokens), static_cast<int>(heads), static_cast<int>(chunk),
+                             static_cast<int>(flags), static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

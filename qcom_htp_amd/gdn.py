@@ -3,6 +3,8 @@
 Mirrors the reference's solve entry points:
 * ``gdn_solve`` -- float32 A [..., C, C] -> T (the fp64 recurrence of
   scripts/gdn_ref_kernel.py:84-87, computed on the GPU in fp32 / bf16-MFMA);
+* ``gdn_chunk_uw`` -- the fused intra-chunk products U = T (beta V), W = T (beta K^) [e^g] of
+  scripts/gdn_ref_kernel.py:71-89 from bf16 keys / values, per-token log decays and betas;
 * ``GdnSolve`` -- the quantized op contract of example/gdn_native/solve_op/src/GdnSolveOp.cpp
   (uint16 codes with zero point and scale on input and output), also the ``gdnbm_solve``
   I/O of example/gdn_native/baremetal/inc/gdnbm.idl:7-13.
@@ -19,7 +21,9 @@ from . import _lib
 FP32 = _lib.QH_GDN_FP32
 BF16 = _lib.QH_GDN_BF16
 
-__all__ = ["gdn_solve", "GdnSolve", "FP32", "BF16"]
+W_DECAY = _lib.QH_GDN_W_DECAY
+
+__all__ = ["gdn_solve", "gdn_chunk_uw", "GdnSolve", "FP32", "BF16", "W_DECAY"]
 
 
 def _stream(stream):
@@ -56,3 +60,27 @@ def GdnSolve(A_codes: torch.Tensor, zpA: int, sA: float, zpT: int, sT: float, pr
                                      float(sT), precision, _stream(stream))
     _lib.check(st, "qh_gdn_solve_u16")
     return out
+
+
+def gdn_chunk_uw(k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor, chunk: int,
+                 decay_w: bool = False, out_dtype: torch.dtype = torch.bfloat16,
+                 stream: Optional[torch.cuda.Stream] = None):
+    """(W, U) [B, T, H, 128] from k, v bf16 [B, T, H, 128] and g (per-token log decay), beta
+    float32 [B, T, H]: U = T (beta v), W = T (beta l2norm(k)) [times e^g when decay_w], with
+    T = (I - A)^-1 of each chunk of ``chunk`` tokens."""
+    for name, x, dt in (("k", k, torch.bfloat16), ("v", v, torch.bfloat16), ("g", g, torch.float32),
+                        ("beta", beta, torch.float32)):
+        if x.device.type != "cuda" or x.dtype != dt or not x.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous {dt} CUDA tensor")
+    if k.dim() != 4 or v.shape != k.shape or g.shape != k.shape[:3] or beta.shape != k.shape[:3]:
+        raise ValueError("k, v: [B, T, H, D]; g, beta: [B, T, H]")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("out_dtype must be bfloat16 or float32")
+    B, T, H, D = k.shape
+    w = torch.empty((B, T, H, D), dtype=out_dtype, device=k.device)
+    u = torch.empty_like(w)
+    flags = (W_DECAY if decay_w else 0) | (_lib.QH_GDN_OUT_F32 if out_dtype == torch.float32 else 0)
+    st = _lib.lib().qh_gdn_chunk_uw(k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), w.data_ptr(),
+                                    u.data_ptr(), B, T, H, D, chunk, flags, _stream(stream))
+    _lib.check(st, "qh_gdn_chunk_uw")
+    return w, u

@@ -97,3 +97,75 @@ def test_gdn_u16_code_contract(gpu, precision):
     tol = 5e-4 if precision == 0 else BF16_TOL
     assert err <= tol, f"oc={err:.3e}"
     assert np.all(Tq.cpu().numpy()[:, np.triu_indices(C, 1)[0], np.triu_indices(C, 1)[1]] == 32768)
+
+
+def chunk_inputs(B, T, H, seed):
+    """Config-5 style inputs: k, v ~ N(0,1) rounded to bf16, beta = sigmoid(N(0,1)),
+    gc = logsigmoid(N(0,1) + 3), in the reference kernel's [B, T, H, (D)] layout."""
+    rng = np.random.default_rng(seed)
+
+    def bf16(x):  # float32 -> bf16 bit patterns, round to nearest even
+        u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    kb = bf16(rng.standard_normal((B, T, H, 128)))
+    vb = bf16(rng.standard_normal((B, T, H, 128)))
+    beta = (1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H))))).astype(np.float32)
+    gc = (-np.logaddexp(0.0, -(rng.standard_normal((B, T, H)) + 3.0))).astype(np.float32)
+    return kb, vb, beta, gc
+
+
+def bf16_to_f64(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("C", [64, 128, 256])
+@pytest.mark.parametrize("decay_w", [False, True], ids=["W_beta_k", "W_beta_k_eg"])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_gdn_chunk_uw_matches_fp64(gpu, C, decay_w, out):
+    """U = T (beta V), W = T (beta K^) [e^g] per chunk and head, against float64 (A built
+    from the same bf16 inputs, T by LAPACK); bound 1.05e-2 relative Frobenius per chunk-head."""
+    import torch
+
+    from qcom_htp_amd.gdn import gdn_chunk_uw
+
+    B, H, nch = 2, 3, 2
+    T = nch * C
+    kb, vb, beta, gc = chunk_inputs(B, T, H, seed=C + 7 * decay_w)
+    print(f"[gdn] chunk_uw C={C} decay_w={decay_w} out={out}", flush=True)
+    dev = gpu
+    kt = torch.from_numpy(kb.view(np.int16)).to(dev).view(torch.bfloat16)
+    vt = torch.from_numpy(vb.view(np.int16)).to(dev).view(torch.bfloat16)
+    w, u = gdn_chunk_uw(kt, vt, torch.from_numpy(gc).to(dev), torch.from_numpy(beta).to(dev), C, decay_w=decay_w,
+                        out_dtype=torch.bfloat16 if out == "bf16" else torch.float32)
+    torch.cuda.synchronize()
+    w = w.float().cpu().numpy().astype(np.float64)
+    u = u.float().cpu().numpy().astype(np.float64)
+    k64, v64 = bf16_to_f64(kb), bf16_to_f64(vb)
+    worst = 0.0
+    for b in range(B):
+        for c in range(nch):
+            sl = slice(c * C, (c + 1) * C)
+            for h in range(H):
+                kc, vc = k64[b, sl, h], v64[b, sl, h]
+                bc, gcc = beta[b, sl, h].astype(np.float64), gc[b, sl, h].astype(np.float64)
+                Tm = og.inverse_fp64(og.build_A(kc, bc, gcc))
+                U, W = og.chunk_uw(Tm, kc, vc, bc, gcc, decay_w=decay_w)
+                eu, ew = og.oc(u[b, sl, h], U), og.oc(w[b, sl, h], W)
+                worst = max(worst, eu, ew)
+                assert eu <= BF16_TOL and ew <= BF16_TOL, f"b={b} chunk={c} h={h}: oc(U)={eu:.3e} oc(W)={ew:.3e}"
+    print(f"[gdn] chunk_uw C={C} worst oc {worst:.3e}", flush=True)
+
+
+def test_gdn_chunk_uw_rejects_bad_shapes(gpu):
+    import torch
+
+    from qcom_htp_amd import _lib
+    from qcom_htp_amd.gdn import gdn_chunk_uw
+
+    k = torch.zeros((1, 96, 2, 128), dtype=torch.bfloat16, device=gpu)
+    g = torch.zeros((1, 96, 2), dtype=torch.float32, device=gpu)
+    with pytest.raises(_lib.QhtpError):
+        gdn_chunk_uw(k, k, g, g, 64)  # 96 tokens is not a multiple of the 64-token chunk
+    with pytest.raises(_lib.QhtpError):
+        gdn_chunk_uw(k, k, g, g, 32)  # unsupported chunk

@@ -93,3 +93,23 @@ def test_int16_block_model_matches_reference_c(tmp_path):
         np.testing.assert_allclose(T_py, T_ref[h], rtol=0, atol=1e-12)
         # and the model is a faithful inverse at its int16 precision
         assert og.oc(T_py, og.inverse_fp64(codes[h].astype(np.float64) * np.float32(sAs[h]))) < 5e-4
+
+
+def test_chunk_uw_solves_the_triangular_system():
+    """U and W from chunk_uw satisfy (I - A) U = beta V and (I - A) W = beta K^ (e^g)."""
+    rng = np.random.default_rng(3)
+    C = 32
+    k = rng.standard_normal((C, 128))
+    v = rng.standard_normal((C, 128))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal(C)))
+    gc = -np.logaddexp(0.0, -(rng.standard_normal(C) + 3.0))
+    A = og.build_A(k, beta, gc)
+    T = og.inverse_fp64(A)
+    ImA = np.eye(C) - A
+    for decay_w in (False, True):
+        U, W = og.chunk_uw(T, k, v, beta, gc, decay_w=decay_w)
+        np.testing.assert_allclose(ImA @ U, beta[:, None] * v, rtol=0, atol=1e-10)
+        kb = beta[:, None] * og.l2norm(k)
+        if decay_w:
+            kb = kb * np.exp(np.cumsum(gc))[:, None]
+        np.testing.assert_allclose(ImA @ W, kb, rtol=0, atol=1e-10)
