@@ -127,6 +127,29 @@ def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
             "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12}, A
 
 
+def gdn_chunk_workload(B: int, T: int, H: int, C: int, steps: int, warmup: int):
+    """Fused chunk products W, U (bf16 out) from bf16 K, V at [B, T, H, 128]."""
+    import torch
+
+    from qcom_htp_amd.gdn import gdn_chunk_uw
+
+    D = 128
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    k = torch.randn((B, T, H, D), generator=gen, device=dev).to(torch.bfloat16)
+    v = torch.randn((B, T, H, D), generator=gen, device=dev).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn((B, T, H), generator=gen, device=dev))
+    gc = torch.nn.functional.logsigmoid(torch.randn((B, T, H), generator=gen, device=dev) + 3.0)
+    wall, ev = time_kernel(lambda i: gdn_chunk_uw(k, v, gc, beta, C), steps, warmup)
+    chunk_heads = B * (T // C) * H
+    # dense algorithmic work per chunk-head: A = K K^T (2 C^2 D), inverse (2/3 C^3), W and U (2 C^2 D each)
+    flops = chunk_heads * (3 * 2.0 * C * C * D + (2.0 / 3.0) * C ** 3)
+    nbytes = B * T * H * (4 * D * 2 + 2 * 4)  # K, V in + W, U out (bf16) + beta, g (fp32)
+    return {"B": B, "T": T, "H": H, "C": C, "ms": ev, "wall_ms": wall, "chunk_heads_per_s": chunk_heads / (ev * 1e-3),
+            "tflops_alg": flops / (ev * 1e-3) / 1e12, "bytes": nbytes, "gbs": nbytes / (ev * 1e-3) / 1e9}
+
+
 def cpu_baseline(case, gdn_A):
     """The oracle (numpy/LAPACK restatement of the reference's CPU path) on host cores."""
     import numpy as np
@@ -206,6 +229,9 @@ def main() -> int:
             log(f"gdn C=256 x 32 heads precision={prec}")
             r, gdn_A = gdn_workload(32, 256, 50, 5, prec)
             extra[f"gdn_c256_h32_{r['precision']}"] = r
+        for C in (64, 256):
+            log(f"gdn chunk W/U B=8 T=4096 H=32 C={C}")
+            extra[f"gdn_chunk_uw_c{C}"] = gdn_chunk_workload(8, 4096, 32, C, 10, 2)
     torch.cuda.synchronize()
 
     tops = prim["tops"]
