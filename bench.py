@@ -191,12 +191,41 @@ def cpu_baseline(case, gdn_A):
     }
 
 
+def copy_calibration() -> int:
+    """A plain streaming kernel of known HBM traffic: bitwise_not over 1 GiB of int32
+    (reads 1 GiB, writes 1 GiB), five launches.  The FETCH_SIZE / WRITE_SIZE counters of
+    these launches give the factor that converts the counters' units into bytes."""
+    import torch
+
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.int32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        torch.bitwise_not(a, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_kernel": "bitwise_not int32", "read_bytes": 4 * n, "write_bytes": 4 * n}), flush=True)
+    return 0
+
+
+def measured_traffic(kernel_key: str):
+    """HBM bytes per launch of a kernel from the committed counter summary (profiles/traffic.json:
+    FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the copy-kernel factor), or None."""
+    p = ROOT / "profiles" / "traffic.json"
+    try:
+        d = json.loads(p.read_text())
+        return d["kernels"][kernel_key]["traffic_bytes"]
+    except Exception:
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="primary line only (no extras, no CPU baseline)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain streaming kernel of known size (for scaling HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no multi-GPU path); run with --gpus 1", file=sys.stderr)
@@ -208,6 +237,8 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
     torch.cuda.init()
+    if args.copy_calibration:
+        return copy_calibration()
 
     M = K = N = 4096
     log("primary: w4a8_per_channel GEMM 4096^3")
@@ -251,7 +282,7 @@ def main() -> int:
         "config": {"workload": "w4a8_per_channel quantized GEMM, u8 act x int4 weight -> u8, M=K=N=4096",
                    "m": M, "k": K, "n": N, "family": "w4a8_per_channel"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": I8_PEAK_TOPS, "unit": "TOPS",
-                     "frac": round(tops / I8_PEAK_TOPS, 4), "traffic": None,
+                     "frac": round(tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("w4a8_gemm_4096"),
                      "kernel": "qmm_gemm_kernel<A8, int4 tiles>", "measured": "stream events over the timed steps"},
         "extra": extra,
     }
