@@ -66,7 +66,7 @@ qh_status qh_qmm_run_path(const qh_qmm_prepared *prep, uint32_t m, const void *a
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: activation rows must be 16-byte aligned");
   if (path > 2) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: unknown path %u", path);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool gemv = path == 2 || (path == 0 && m <= 16);
+  const bool gemv = path == 2 || (path == 0 && m <= 16 && gemv_fits(prep, static_cast<int>(m)));
   if (gemv) return launch_qmm_gemv(prep, static_cast<int>(m), act_dev, out_dev, s);
   return launch_qmm_gemm(prep, static_cast<int>(m), act_dev, out_dev, s);
 }

@@ -3,16 +3,25 @@
 //
 // Weight stream layout (prepared once): [N/16 column groups][K/32 k-groups][16 columns][bytes],
 // 16 B per (column, k-group) for int4 (byte j: low nibble k=j, high nibble k=j+16,
-// offset-binary) or 32 B for int8.  One wave instruction therefore reads 4 k-groups x 16 columns
-// = 1 KiB (int4) / 2 KiB (int8) of contiguous HBM.  LPBQ block scales are streamed as
-// [N/16][K/block][16] bytes and applied to each k-group's integer partial dot product
-// (sum_k a*(q*f) = f * sum_k a*q inside a block), which keeps the integer result exact.
+// offset-binary u = code + 8) or 32 B for int8.  One wave instruction reads 4 k-groups x 16
+// columns = 1 KiB (int4) / 2 KiB (int8) of contiguous HBM.  LPBQ block scales are streamed as
+// [N/16][K/block][16] bytes and read by each lane beside its weight words.
 //
-// Activations (M x K) are staged once per workgroup in LDS as signed int8 planes
-// (a - 128 for 8-bit; hi / lo' bytes of a - 32768 for 16-bit).  For 16-bit activations the
-// workgroup also forms R1[m] = sum_k |a - zp|, which bounds the float32-rounding residue term
-// of the requantisation (the GEMV does not stream the residue plane).  The epilogue and the
-// exact fixup follow the GEMM's (qmm_gemm.hip).
+// Work split: a workgroup (4 waves) owns one 16-column group at a time and splits its K
+// between all 256 lanes: lane (sub, col) of wave w takes the k-groups kg = 4 (w + 4 i) + sub,
+// so every wave instruction is one contiguous KiB and a lane issues all of its loads (8 at
+// K = 4096) before it uses any.  With one group per workgroup every byte of the matrix is
+// requested at once, which is what an HBM-bound stream needs.
+//
+// Arithmetic: activations are staged once per workgroup in LDS as signed int8 planes
+// (a - 128 for 8-bit; hi / lo' bytes of a - 32768 for 16-bit) together with their sums over
+// each 32-k group.  Int4 codes are used as the unsigned nibble u = code + 8 (a mask, no sign
+// extension): sum_k a'_k (u_k - 8) f = f (dot4(a', u) - 8 sum_k a'_k) per k-group, exact in
+// int32 (f = the LPBQ block scale, 1 otherwise).  The four waves' partial sums meet in LDS;
+// each output is then requantised by one thread with the GEMM's rounding rules (t in float64,
+// exact fixup of outputs within the certified margin of a rounding boundary).
+
+#include <atomic>
 
 #include "qmm_internal.h"
 
@@ -20,18 +29,22 @@ namespace qh {
 namespace {
 
 constexpr int kGemvThreads = 256;
-constexpr int kGemvMaxLds = 128 * 1024;  // activation planes
+constexpr int kGemvWaves = kGemvThreads / 64;
+constexpr int kGemvMaxDynLds = 148 * 1024;  // activation planes + k-group sums
+constexpr int kU = kGemvKU;                  // k-groups per lane per batch (loads in flight)
 
 struct GemvArgs {
   const uint8_t *act;
   void *out;
   const uint8_t *w;      // GEMV stream
-  const uint8_t *lpbq;   // [N/16][K/bs][16]
+  const uint8_t *lpbq;   // block scales, gemv_scale_index layout
   const double *alpha, *beta, *margin, *absb, *bias_deq, *mr1;
   const int64_t *corr, *mant, *colsum;
   const float *s32;
-  int M, N, K, KG, nblk, bs_shift;
+  int M, N, K, KG, nbatch, sub_shift;
   int act_zp, out_zp, out_qmax, out16;
+  int off_asum;  // byte offset of the k-group sums in dynamic LDS
+  int off_fixw;  // byte offset of the fixup columns' weight words (register-held fixup)
   double sA, sO;
 };
 
@@ -39,50 +52,67 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// Integer weight codes (times the LPBQ block scale) of column n, k-group kg: 32 values.
-template <int FMT, bool LPBQ>
-__device__ __forceinline__ void load_w32(const GemvArgs &g, int n, int kg, int (&w)[32]) {
-  const size_t base = (static_cast<size_t>(n / 16) * g.KG + kg) * 16 + (n % 16);
-  if (FMT == kTileI4) {
-    uint4 v = *reinterpret_cast<const uint4 *>(g.w + base * 16);
-    const uint8_t *b = reinterpret_cast<const uint8_t *>(&v);
-    int f = 1;
-    if (LPBQ) f = g.lpbq[(static_cast<size_t>(n / 16) * g.nblk + ((kg * 32) >> g.bs_shift)) * 16 + (n % 16)];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      w[j] = ((b[j] & 15) - 8) * f;
-      w[j + 16] = ((b[j] >> 4) - 8) * f;
-    }
-  } else {
-    const uint4 *p = reinterpret_cast<const uint4 *>(g.w + base * 32);
-    uint4 v0 = p[0], v1 = p[1];
-    const int8_t *b0 = reinterpret_cast<const int8_t *>(&v0), *b1 = reinterpret_cast<const int8_t *>(&v1);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      w[j] = b0[j];
-      w[j + 16] = b1[j];
-    }
-  }
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS operations
+// only.  __syncthreads() would also wait for every global load in flight (its release fence),
+// which would hold the staging and the reductions behind the weight stream.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Streaming load that bypasses cache retention (the weights are read once per call).
+__device__ __forceinline__ uint4 load_stream(const uint8_t *p) {
+  const v4u x = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+  return make_uint4(x.x, x.y, x.z, x.w);
 }
 
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// sum of the four signed bytes of x
+__device__ __forceinline__ int bsum4(uint32_t x, int c) { return sdot4(x, 0x01010101u, c); }
+
+// Exact float64 recomputation of output (m, n) by a whole wave, term by term as the reference
+// oracle forms it: sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), + bias_deq, / sO, + out_zp.
+// The activations come from the staged LDS planes.
+// Kept lean on purpose: the kernel's register budget is the maximum over all of its code, and
+// this rare path must not lower the occupancy of the stream.
 template <bool A16, int FMT, bool LPBQ>
-__device__ void gemv_fixup(const GemvArgs &g, int m, int n, int lane) {
+__device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, int lane) {
+  constexpr int WB = FMT == kTileI4 ? 16 : 32;
   const float sc = g.s32[n];
+  const int K = g.K, KG = g.KG;
+  const uint8_t *const wcol = g.w + (static_cast<size_t>(n / 16) * KG * 16 + (n % 16)) * WB;
+  // a - zp = plane value + off (8-bit: a - 128; 16-bit: 256 hi + lo' with a - 32768 - 128)
+  const int off = (A16 ? 32768 + 128 : 128) - g.act_zp;
   double s = 0.0;
-  for (int kg = lane; kg < g.KG; kg += 64) {
-    int w[32];
-    load_w32<FMT, LPBQ>(g, n, kg, w);
-    const int k = kg * 32;
+  for (int kg = lane; kg < KG; kg += 64) {
+    uint32_t wd[WB / 4];
+    const uint4 *p = reinterpret_cast<const uint4 *>(wcol + static_cast<size_t>(kg) * 16 * WB);
 #pragma unroll
+    for (int q = 0; q < WB / 16; ++q) {
+      const uint4 v = p[q];
+      wd[4 * q] = v.x; wd[4 * q + 1] = v.y; wd[4 * q + 2] = v.z; wd[4 * q + 3] = v.w;
+    }
+    const int f = LPBQ ? g.lpbq[gemv_scale_index_kg(n, kg, g.nbatch, g.sub_shift)] : 1;
+    const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * K + kg * 32);
+    const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * K + kg * 32);
+#pragma unroll 4
     for (int j = 0; j < 32; ++j) {
-      const int a = A16 ? reinterpret_cast<const uint16_t *>(g.act)[static_cast<size_t>(m) * g.K + k + j]
-                        : g.act[static_cast<size_t>(m) * g.K + k + j];
-      const float wd = static_cast<float>(w[j]) * sc;
-      s = fma(static_cast<double>(a - g.act_zp) * g.sA, static_cast<double>(wd), s);
+      int w;
+      if (FMT == kTileI4) {
+        const uint32_t byte = (wd[(j & 15) >> 2] >> (8 * (j & 3))) & 0xFFu;
+        w = ((j < 16 ? (byte & 15u) : (byte >> 4)) - 8) * f;
+      } else {
+        w = static_cast<int8_t>((wd[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+      }
+      const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : static_cast<int>(hp[j])) + off;
+      const float wf = static_cast<float>(w) * sc;
+      s = fma(static_cast<double>(a) * g.sA, static_cast<double>(wf), s);
     }
   }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
   if (lane == 0) {
     const double t = (s + g.bias_deq[n]) / g.sO + static_cast<double>(g.out_zp);
     const double o = fmin(fmax(rint(t), 0.0), static_cast<double>(g.out_qmax));
@@ -94,208 +124,437 @@ __device__ void gemv_fixup(const GemvArgs &g, int m, int n, int lane) {
   }
 }
 
-template <bool A16, int FMT, bool LPBQ, int MM>
-__global__ __launch_bounds__(kGemvThreads) void qmm_gemv_kernel(GemvArgs g) {
-  extern __shared__ uint4 smem[];
-  uint8_t *act_lds = reinterpret_cast<uint8_t *>(smem);  // [planes][M][K] int8
-  __shared__ uint32_t r1[16];
-
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int M = g.M, K = g.K;
-  if (t < 16) r1[t] = 0;
-  __syncthreads();
-
-  // ---- stage activations as signed int8 planes ---------------------------------------
-  if (!A16) {
-    const int chunks = M * K / 16;
-    for (int c = t; c < chunks; c += kGemvThreads) {
-      uint4 v = reinterpret_cast<const uint4 *>(g.act)[c];
-      v.x ^= 0x80808080u;
-      v.y ^= 0x80808080u;
-      v.z ^= 0x80808080u;
-      v.w ^= 0x80808080u;
-      reinterpret_cast<uint4 *>(act_lds)[c] = v;
-    }
-  } else {
-    const int chunks = M * K / 8;  // 8 values per 16 B
-    uint2 *hi_pl = reinterpret_cast<uint2 *>(act_lds);
-    uint2 *lo_pl = reinterpret_cast<uint2 *>(act_lds + static_cast<size_t>(M) * K);
-    for (int c = t; c < chunks; c += kGemvThreads) {
-      uint4 v = reinterpret_cast<const uint4 *>(g.act)[c];
-      const uint16_t *h = reinterpret_cast<const uint16_t *>(&v);
-      uint32_t sum = 0;
+// Exact float64 recomputation of up to kFixBatch outputs at once by the whole workgroup, from
+// weights that the workgroup already holds: entry e's column weight words and LPBQ scales sit
+// in LDS at fixw + e KG WB ([KG][WB bytes]) and fixs + e KG ([KG]), the activations in the
+// staged planes.  Thread t takes 16 terms of each of its (k-group, half) pairs for every entry
+// (independent accumulation chains); the partial sums meet in LDS.
+constexpr int kFixBatch = 8;
+template <bool A16, int FMT, bool LPBQ>
+__device__ void gemv_fixup_batch(const GemvArgs &g, const uint8_t *lds, const uint8_t *fixw, const uint8_t *fixs,
+                                 double *dred, const uint16_t *list, int nb, int grp, int t) {
+  constexpr int WB = FMT == kTileI4 ? 16 : 32;
+  const int K = g.K, KG = g.KG;
+  const int off = (A16 ? 32768 + 128 : 128) - g.act_zp;
+  double s[kFixBatch];
+  float sc[kFixBatch];
+  int mrow[kFixBatch];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sum += static_cast<uint32_t>(abs(static_cast<int>(h[j]) - g.act_zp));
-      v.x ^= 0x80808080u;
-      v.y ^= 0x80808080u;
-      v.z ^= 0x80808080u;
-      v.w ^= 0x80808080u;
-      hi_pl[c] = make_uint2(perm(v.y, v.x, 0x07050301u), perm(v.w, v.z, 0x07050301u));
-      lo_pl[c] = make_uint2(perm(v.y, v.x, 0x06040200u), perm(v.w, v.z, 0x06040200u));
-      atomicAdd(&r1[(c * 8) / K], sum);
+  for (int e = 0; e < kFixBatch; ++e) {
+    s[e] = 0.0;
+    const int tt = list[e < nb ? e : 0];
+    mrow[e] = tt >> 4;
+    sc[e] = g.s32[grp * 16 + (tt & 15)];
+  }
+  for (int u = t; u < 2 * KG; u += kGemvThreads) {
+    const int kg = u >> 1, h = u & 1;  // terms k = 32 kg + 16 h + j, j < 16
+#pragma unroll
+    for (int e = 0; e < kFixBatch; ++e) {
+      if (e >= nb) break;
+      const uint4 v = *reinterpret_cast<const uint4 *>(fixw + (static_cast<size_t>(e) * KG + kg) * WB +
+                                                       (FMT == kTileI4 ? 0 : 16 * h));
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+      const int f = LPBQ ? fixs[e * KG + kg] : 1;
+      const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(mrow[e]) * K + kg * 32 + 16 * h);
+      const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + mrow[e]) * K + kg * 32 + 16 * h);
+#pragma unroll 4
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = (wd[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        const int w = FMT == kTileI4 ? ((h ? (byte >> 4) : (byte & 15u)) - 8) * f : static_cast<int8_t>(byte);
+        const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : static_cast<int>(hp[j])) + off;
+        const float wf = static_cast<float>(w) * sc[e];
+        s[e] = fma(static_cast<double>(a) * g.sA, static_cast<double>(wf), s[e]);
+      }
     }
   }
-  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kFixBatch; ++e) {
+    if (e >= nb) break;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s[e] += __shfl_xor(s[e], o, 64);
+    if ((t & 63) == 0) dred[e * kGemvWaves + (t >> 6)] = s[e];
+  }
+  lds_barrier();
+  if (t < nb) {
+    const int tt = list[t];
+    const int m = tt >> 4, n = grp * 16 + (tt & 15);
+    const double tot = dred[t * kGemvWaves] + dred[t * kGemvWaves + 1] + dred[t * kGemvWaves + 2] + dred[t * kGemvWaves + 3];
+    const double tv = (tot + g.bias_deq[n]) / g.sO + static_cast<double>(g.out_zp);
+    const double o = fmin(fmax(rint(tv), 0.0), static_cast<double>(g.out_qmax));
+    const size_t idx = static_cast<size_t>(m) * g.N + n;
+    if (g.out16)
+      static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(o);
+    else
+      static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(o);
+  }
+}
 
+// Staging of the activations, one (row, k-group) unit of 32 values at a time: the signed
+// plane bytes and (int4 weights) the plane sums over the unit.  16-bit activations also add
+// sum |a - zp| of each row into r1 (the bound of the float32-rounding residue term in the
+// margin).  Loading and storing are separate so that the first unit's load can be issued
+// ahead of the weight stream.
+template <bool A16>
+struct ActUnit {
+  uint4 v[A16 ? 4 : 2];
+};
+
+template <bool A16>
+__device__ __forceinline__ void load_unit(const GemvArgs &g, int u, ActUnit<A16> &r) {
+  const int m = u / g.KG, kg = u - m * g.KG;
+  const uint4 *src = A16 ? reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(g.act) + static_cast<size_t>(m) * g.K + kg * 32)
+                         : reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(m) * g.K + kg * 32);
+#pragma unroll
+  for (int q = 0; q < (A16 ? 4 : 2); ++q) r.v[q] = src[q];
+}
+
+template <bool A16, int FMT>
+__device__ __forceinline__ void store_unit(const GemvArgs &g, int u, ActUnit<A16> r, uint8_t *lds, uint32_t *r1) {
+  const int M = g.M, K = g.K, KG = g.KG;
+  const int m = u / KG, kg = u - m * KG;
+  int16_t *asum = reinterpret_cast<int16_t *>(lds + g.off_asum);
+  if (!A16) {
+    uint4 v0 = r.v[0], v1 = r.v[A16 ? 1 : 1];
+    v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
+    v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
+    uint4 *dst = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(m) * K + kg * 32);
+    dst[0] = v0;
+    dst[1] = v1;
+    if (FMT == kTileI4) {
+      int s = bsum4(v0.x, 0);
+      s = bsum4(v0.y, s); s = bsum4(v0.z, s); s = bsum4(v0.w, s);
+      s = bsum4(v1.x, s); s = bsum4(v1.y, s); s = bsum4(v1.z, s); s = bsum4(v1.w, s);
+      asum[u] = static_cast<int16_t>(s);
+    }
+  } else {
+    uint32_t hv[8], lv[8];
+    uint32_t rs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint4 v = r.v[q & (A16 ? 3 : 1)];
+      const uint16_t *h = reinterpret_cast<const uint16_t *>(&v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rs += static_cast<uint32_t>(abs(static_cast<int>(h[j]) - g.act_zp));
+      v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+      hv[2 * q] = perm(v.y, v.x, 0x07050301u);
+      hv[2 * q + 1] = perm(v.w, v.z, 0x07050301u);
+      lv[2 * q] = perm(v.y, v.x, 0x06040200u);
+      lv[2 * q + 1] = perm(v.w, v.z, 0x06040200u);
+    }
+    uint4 *dh = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(m) * K + kg * 32);
+    uint4 *dl = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(M + m) * K + kg * 32);
+    dh[0] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+    dh[1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+    dl[0] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+    dl[1] = make_uint4(lv[4], lv[5], lv[6], lv[7]);
+    if (FMT == kTileI4) {
+      int sh = 0, sl = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        sh = bsum4(hv[j], sh);
+        sl = bsum4(lv[j], sl);
+      }
+      asum[u] = static_cast<int16_t>(sh);
+      asum[M * KG + u] = static_cast<int16_t>(sl);
+    }
+    atomicAdd(&r1[m], rs);
+  }
+}
+
+template <bool A16, int FMT, bool LPBQ, int MM>
+__global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kernel(const GemvArgs g) {
+  extern __shared__ uint4 smem[];
+  uint8_t *const lds = reinterpret_cast<uint8_t *>(smem);
+  __shared__ int red[kGemvWaves][MM][16];
+  __shared__ int red2[A16 ? kGemvWaves : 1][A16 ? MM : 1][16];
+  __shared__ uint32_t r1[16];
+  __shared__ uint16_t fix_list[MM * 16];
+  __shared__ int fix_cnt;
+  __shared__ double dred[kFixBatch * kGemvWaves];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int M = g.M, K = g.K, KG = g.KG;
+  constexpr int WB = FMT == kTileI4 ? 16 : 32;  // stream bytes per (column, k-group)
+  const int16_t *const asum = reinterpret_cast<const int16_t *>(lds + g.off_asum);
+  const int col = lane & 15, sub = lane >> 4;
   const int groups = g.N / 16;
-  const int waves_total = gridDim.x * (kGemvThreads / 64);
-  const int col = lane & 15, sub = lane >> 4;  // 4 k-groups per wave instruction
-  for (int grp = blockIdx.x * (kGemvThreads / 64) + wave; grp < groups; grp += waves_total) {
-    const int n = grp * 16 + col;
+  const int iters = (KG + 15) / 16;  // k-group slots per lane (some past KG when KG % 16 != 0)
+  // One batch of kU k-groups per lane: the weight words and their LPBQ block scales (one
+  // 8-byte load of the lane's kU scales).
+  uint4 wv[kU][FMT == kTileI4 ? 1 : 2];
+  uint2 fsv = make_uint2(0x01010101u, 0x01010101u);
+  // Straight-line loads (indices clamped, results of slots past KG discarded) keep every load
+  // of a batch in one basic block, so they issue back to back and their waits count down.
+  auto issue = [&](int grp, int i0) {
+    const uint8_t *const wgrp = g.w + static_cast<size_t>(grp) * KG * 16 * WB;
+    if (LPBQ)  // first: slot 0 needs it, and loads complete in order
+      fsv = *reinterpret_cast<const uint2 *>(g.lpbq + gemv_scale_index(grp, i0 / kU, g.nbatch, wave, sub >> g.sub_shift,
+                                                                       4 >> g.sub_shift, col, 0));
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+      const int kg = min(4 * (wave + 4 * (i0 + i)) + sub, KG - 1);
+      const uint8_t *p = wgrp + (static_cast<size_t>(kg) * 16 + col) * WB;
+      wv[i][0] = load_stream(p);
+      if (FMT != kTileI4) wv[i][FMT == kTileI4 ? 0 : 1] = load_stream(p + 16);
+    }
+  };
+  // Per-output epilogue constants of thread t's output (row t / 16, column t % 16 of the
+  // group), requested together with the group's first batch of weights.
+  struct Epi {
+    double alpha, beta, margin, absb, mr1;
+    int64_t corr, mant;
+  } ep{};
+  const bool owns_out = t < MM * 16 && (t >> 4) < M;
+  auto load_epi = [&](int grp) {  // every thread loads (its column exists), only owners use it
+    const int n = grp * 16 + (t & 15);
+    ep.alpha = g.alpha[n];
+    ep.beta = g.beta[n];
+    ep.margin = g.margin[n];
+    ep.absb = g.absb[n];
+    if (A16) {
+      ep.corr = g.colsum[n];
+      ep.mr1 = g.mr1[n];
+      ep.mant = g.mant[n];
+    } else {
+      ep.corr = g.corr[n];
+    }
+  };
+  // The first activation unit and the first batch of weights are requested before anything
+  // waits: the staging then overlaps the weight stream.
+  ActUnit<A16> au;
+  const int units = M * KG;
+  load_unit<A16>(g, min(t, units - 1), au);
+  issue(blockIdx.x, 0);  // the launch never has more workgroups than groups
+  load_epi(blockIdx.x);
+  if (t < 16) r1[t] = 0;
+  if (t == 0) fix_cnt = 0;
+  lds_barrier();
+  if (t < units) store_unit<A16, FMT>(g, t, au, lds, r1);
+  for (int u = t + kGemvThreads; u < units; u += kGemvThreads) {
+    load_unit<A16>(g, u, au);
+    store_unit<A16, FMT>(g, u, au, lds, r1);
+  }
+  lds_barrier();
+
+  // Workgroups loop over groups only for 16 rows (whose staging is amortised over several
+  // groups); otherwise each workgroup owns exactly one group.
+  constexpr bool kLoop = MM == 16;
+  for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
     int acc[MM], acc2[A16 ? MM : 1];
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
       acc[m] = 0;
       if (A16) acc2[m] = 0;
     }
-    const uint8_t *wbase = g.w + static_cast<size_t>(grp) * g.KG * 16 * (FMT == kTileI4 ? 16 : 32);
-    for (int kg = sub; kg < g.KG; kg += 4) {
-      uint32_t w[8];
-      if (FMT == kTileI4) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(wbase + (static_cast<size_t>(kg) * 16 + col) * 16);
-        const uint32_t m4 = 0x0F0F0F0Fu;
-        w[0] = ((v.x & m4) + 0x78787878u) ^ 0x80808080u;
-        w[1] = ((v.y & m4) + 0x78787878u) ^ 0x80808080u;
-        w[2] = ((v.z & m4) + 0x78787878u) ^ 0x80808080u;
-        w[3] = ((v.w & m4) + 0x78787878u) ^ 0x80808080u;
-        w[4] = (((v.x >> 4) & m4) + 0x78787878u) ^ 0x80808080u;
-        w[5] = (((v.y >> 4) & m4) + 0x78787878u) ^ 0x80808080u;
-        w[6] = (((v.z >> 4) & m4) + 0x78787878u) ^ 0x80808080u;
-        w[7] = (((v.w >> 4) & m4) + 0x78787878u) ^ 0x80808080u;
-      } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(wbase + (static_cast<size_t>(kg) * 16 + col) * 32);
-        const uint4 v0 = p[0], v1 = p[1];
-        w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
-        w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
-      }
-      int f = 1;
-      if (LPBQ) f = g.lpbq[(static_cast<size_t>(grp) * g.nblk + ((kg * 32) >> g.bs_shift)) * 16 + col];
+    for (int i0 = 0; i0 < iters; i0 += kU) {
+      if (i0 > 0) issue(grp, i0);
 #pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        if (MM == 1 || m < M) {  // predicated: MM is a compile-time trip count
-        const uint4 *ap = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(m) * K + kg * 32);
-        const uint4 a0 = ap[0], a1 = ap[1];
-        int d = 0;
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a0.x), static_cast<int>(w[0]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a0.y), static_cast<int>(w[1]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a0.z), static_cast<int>(w[2]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a0.w), static_cast<int>(w[3]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a1.x), static_cast<int>(w[4]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a1.y), static_cast<int>(w[5]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a1.z), static_cast<int>(w[6]), d, false);
-        d = __builtin_amdgcn_sdot4(static_cast<int>(a1.w), static_cast<int>(w[7]), d, false);
-        acc[m] += LPBQ ? d * f : d;
-        if (A16) {
-          const uint4 *lp = reinterpret_cast<const uint4 *>(act_lds + static_cast<size_t>(M + m) * K + kg * 32);
-          const uint4 b0 = lp[0], b1 = lp[1];
-          int e = 0;
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b0.x), static_cast<int>(w[0]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b0.y), static_cast<int>(w[1]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b0.z), static_cast<int>(w[2]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b0.w), static_cast<int>(w[3]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b1.x), static_cast<int>(w[4]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b1.y), static_cast<int>(w[5]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b1.z), static_cast<int>(w[6]), e, false);
-          e = __builtin_amdgcn_sdot4(static_cast<int>(b1.w), static_cast<int>(w[7]), e, false);
-          acc2[m] += LPBQ ? e * f : e;
+      for (int i = 0; i < kU; ++i) {
+        const int kg_raw = 4 * (wave + 4 * (i0 + i)) + sub;
+        const bool valid = kg_raw < KG;  // slot past the end of K: zero weights
+        const int kg = valid ? kg_raw : KG - 1;
+        uint32_t w[8];
+        if (FMT == kTileI4) {
+          const uint4 v = wv[i][0];
+          const uint32_t m4 = valid ? 0x0F0F0F0Fu : 0u;
+          w[0] = v.x & m4; w[1] = v.y & m4; w[2] = v.z & m4; w[3] = v.w & m4;
+          w[4] = (v.x >> 4) & m4; w[5] = (v.y >> 4) & m4; w[6] = (v.z >> 4) & m4; w[7] = (v.w >> 4) & m4;
+        } else {
+          const uint4 v0 = wv[i][0], v1 = wv[i][FMT == kTileI4 ? 0 : 1];
+          const uint32_t mk = valid ? 0xFFFFFFFFu : 0u;
+          w[0] = v0.x & mk; w[1] = v0.y & mk; w[2] = v0.z & mk; w[3] = v0.w & mk;
+          w[4] = v1.x & mk; w[5] = v1.y & mk; w[6] = v1.z & mk; w[7] = v1.w & mk;
         }
+        const int a8 = valid ? 8 : 0;  // the -8 offset of the unsigned nibble codes
+        const int f = LPBQ ? static_cast<int>(((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu) : 1;
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+          if (MM > 1 && m >= M) continue;
+          const uint4 *ap = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(m) * K + kg * 32);
+          const uint4 a0 = ap[0], a1 = ap[1];
+          int d = sdot4(a0.x, w[0], 0);
+          d = sdot4(a0.y, w[1], d); d = sdot4(a0.z, w[2], d); d = sdot4(a0.w, w[3], d);
+          d = sdot4(a1.x, w[4], d); d = sdot4(a1.y, w[5], d); d = sdot4(a1.z, w[6], d); d = sdot4(a1.w, w[7], d);
+          if (FMT == kTileI4) d -= a8 * asum[m * KG + kg];
+          acc[m] += LPBQ ? d * f : d;
+          if (A16) {
+            const uint4 *lp = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(M + m) * K + kg * 32);
+            const uint4 b0 = lp[0], b1 = lp[1];
+            int e = sdot4(b0.x, w[0], 0);
+            e = sdot4(b0.y, w[1], e); e = sdot4(b0.z, w[2], e); e = sdot4(b0.w, w[3], e);
+            e = sdot4(b1.x, w[4], e); e = sdot4(b1.y, w[5], e); e = sdot4(b1.z, w[6], e); e = sdot4(b1.w, w[7], e);
+            if (FMT == kTileI4) e -= a8 * asum[(M + m) * KG + kg];
+            acc2[m] += LPBQ ? e * f : e;
+          }
         }
       }
     }
-    // reduce over the 4 k-group lanes of each column
+    // the next group's first batch is in flight during the reduction and the epilogue
+    if (kLoop && grp + static_cast<int>(gridDim.x) < groups) issue(grp + gridDim.x, 0);
+    // reduce over the 4 k-group lanes of each column, then over the waves in LDS
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
       acc[m] += __shfl_xor(acc[m], 16, 64);
       acc[m] += __shfl_xor(acc[m], 32, 64);
+      if (sub == 0) red[wave][m][col] = acc[m];
       if (A16) {
         acc2[m] += __shfl_xor(acc2[m], 16, 64);
         acc2[m] += __shfl_xor(acc2[m], 32, 64);
+        if (sub == 0) red2[wave][m][col] = acc2[m];
       }
     }
-    // requantise: lanes 0..15 own one column each
-    uint32_t amb_mask = 0;
-    if (sub == 0 && n < g.N) {
-      double alpha = g.alpha[n];
-      const double beta = g.beta[n], margin = g.margin[n], absb = g.absb[n];
-      int64_t corr;
-      double mr1 = 0.0;
-      if (A16) {
-        alpha *= static_cast<double>(g.mant[n]);
-        corr = g.colsum[n] * static_cast<int64_t>(128 + 32768 - g.act_zp);
-        mr1 = g.mr1[n];
-      } else {
-        corr = g.corr[n];
-      }
+    lds_barrier();
+    // requantise: thread t owns output (row t / 16, column t % 16) of the group
+    const int om = t >> 4, n = grp * 16 + (t & 15);
+    bool amb = false;
+    if (owns_out) {
+      int S1 = 0, S2 = 0;
 #pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        const int64_t S = A16 ? 256 * static_cast<int64_t>(acc[m]) + acc2[m] + corr : static_cast<int64_t>(acc[m]) + corr;
-        const double t = fma(static_cast<double>(S), alpha, beta);
-        const double fl = floor(t);
-        const double slack = margin + (A16 ? mr1 * static_cast<double>(r1[m]) : 0.0) + 0x1p-48 * (fabs(t) + absb);
-        const bool near_tie = fabs((t - fl) - 0.5) <= slack;
-        const double lo = fmin(fmax(fl, 0.0), static_cast<double>(g.out_qmax));
-        const double hi = fmin(fmax(fl + 1.0, 0.0), static_cast<double>(g.out_qmax));
-        const bool amb = near_tie && lo != hi;
-        if (m < M && amb) amb_mask |= 1u << m;
-        if (m < M && !amb) {
-          const double o = fmin(fmax(rint(t), 0.0), static_cast<double>(g.out_qmax));
-          const size_t idx = static_cast<size_t>(m) * g.N + n;
-          if (g.out16)
-            static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(o);
-          else
-            static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(o);
+      for (int w = 0; w < kGemvWaves; ++w) {
+        S1 += red[w][om][t & 15];
+        if (A16) S2 += red2[w][om][t & 15];
+      }
+      const double alpha = A16 ? ep.alpha * static_cast<double>(ep.mant) : ep.alpha;
+      const double beta = ep.beta, margin = ep.margin, absb = ep.absb, mr1 = ep.mr1;
+      const int64_t corr = A16 ? ep.corr * static_cast<int64_t>(128 + 32768 - g.act_zp) : ep.corr;
+      const int64_t S = A16 ? 256 * static_cast<int64_t>(S1) + S2 + corr : static_cast<int64_t>(S1) + corr;
+      const double tv = fma(static_cast<double>(S), alpha, beta);
+      const double fl = floor(tv);
+      const double slack = margin + (A16 ? mr1 * static_cast<double>(r1[om]) : 0.0) + 0x1p-48 * (fabs(tv) + absb);
+      const bool near_tie = fabs((tv - fl) - 0.5) <= slack;
+      const double lo = fmin(fmax(fl, 0.0), static_cast<double>(g.out_qmax));
+      const double hi = fmin(fmax(fl + 1.0, 0.0), static_cast<double>(g.out_qmax));
+      amb = near_tie && lo != hi;
+      if (!amb) {
+        const double o = fmin(fmax(rint(tv), 0.0), static_cast<double>(g.out_qmax));
+        const size_t idx = static_cast<size_t>(om) * g.N + n;
+        if (g.out16)
+          static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(o);
+        else
+          static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(o);
+      }
+    }
+    // exact fixup of the ambiguous outputs: listed in LDS, then shared out over the waves
+    if (amb) fix_list[atomicAdd(&fix_cnt, 1)] = static_cast<uint16_t>(t);
+    lds_barrier();
+    const int nfix = fix_cnt;
+    if (kLoop || KG > kGemvBatchKG) {
+      // the weight registers hold the next group or only the last batch: re-read the column
+      for (int e = wave; e < nfix; e += kGemvWaves) {
+        const int tt = fix_list[e];
+        gemv_fixup<A16, FMT, LPBQ>(g, lds, tt >> 4, grp * 16 + (tt & 15), lane);
+      }
+    } else {
+      // the column's weights (one batch: K <= 4096) are still in the registers of its 16
+      // lanes: they hand them over
+      uint8_t *const fixw = lds + g.off_fixw;
+      uint8_t *const fixs = fixw + kFixBatch * KG * WB;
+      for (int e0 = 0; e0 < nfix; e0 += kFixBatch) {
+        const int nb = min(kFixBatch, nfix - e0);
+        for (int e = 0; e < nb; ++e) {
+          if (col != (fix_list[e0 + e] & 15)) continue;
+#pragma unroll
+          for (int i = 0; i < kU; ++i) {
+            const int kg = 4 * (wave + 4 * i) + sub;
+            if (kg < KG) {
+              uint8_t *dst = fixw + (static_cast<size_t>(e) * KG + kg) * WB;
+              *reinterpret_cast<uint4 *>(dst) = wv[i][0];
+              if (FMT != kTileI4) *reinterpret_cast<uint4 *>(dst + 16) = wv[i][FMT == kTileI4 ? 0 : 1];
+              if (LPBQ) fixs[e * KG + kg] = static_cast<uint8_t>(((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu);
+            }
+          }
         }
+        lds_barrier();
+        gemv_fixup_batch<A16, FMT, LPBQ>(g, lds, fixw, fixs, dred, fix_list + e0, nb, grp, t);
+        lds_barrier();  // fixw / dred are rewritten by the next batch
       }
     }
-    // exact fixup of ambiguous outputs, one wave-cooperative dot product each
-    for (int src = 0; src < 16; ++src) {
-      uint32_t mask = __shfl(amb_mask, src, 64);
-      while (mask) {
-        const int m = __ffs(mask) - 1;
-        mask &= mask - 1;
-        gemv_fixup<A16, FMT, LPBQ>(g, m, grp * 16 + src, lane);
-      }
-    }
+    lds_barrier();  // red and the fixup list are rewritten by the next group
+    if (t == 0) fix_cnt = 0;
+    if (!kLoop) break;
+    if (grp + static_cast<int>(gridDim.x) < groups) load_epi(grp + gridDim.x);
   }
 }
 
-template <bool A16, int FMT, bool LPBQ>
-qh_status launch_mm(const GemvArgs &g, hipStream_t stream) {
-  const int planes = A16 ? 2 : 1;
-  const size_t lds = static_cast<size_t>(planes) * g.M * g.K;
-  const int groups = g.N / 16;
-  int blocks = (groups + 3) / 4;
-  if (blocks > 512) blocks = 512;
-  dim3 grid(blocks), block(kGemvThreads);
-#define QH_GEMV_LAUNCH(MMV)                                                                                  \
-  do {                                                                                                       \
-    hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void *>(&qmm_gemv_kernel<A16, FMT, LPBQ, MMV>), \
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds);            \
-    if (e_ != hipSuccess) return hip_fail(e_, "hipFuncSetAttribute(qmm_gemv_kernel)");                       \
-    hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MMV>), grid, block, lds, stream, g);                 \
-  } while (0)
-  if (g.M <= 1)
-    QH_GEMV_LAUNCH(1);
-  else if (g.M <= 4)
-    QH_GEMV_LAUNCH(4);
-  else
-    QH_GEMV_LAUNCH(16);
-#undef QH_GEMV_LAUNCH
-  hipError_t err = hipGetLastError();
+// Raises the kernel's dynamic LDS limit once per device (the call costs a driver round trip,
+// too much for a launch that streams 30 MB in a few microseconds).
+template <class Kernel>
+qh_status allow_dyn_lds(Kernel kernel) {
+  static std::atomic<uint32_t> done{0};  // bit d: set on device d
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  const uint32_t bit = dev < 32 ? 1u << dev : 0u;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return QH_STATUS_OK;
+  e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kGemvMaxDynLds);
+  if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(qmm_gemv_kernel)");
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return QH_STATUS_OK;
+}
+
+template <bool A16, int FMT, bool LPBQ, int MM>
+qh_status launch_one(const GemvArgs &g, dim3 grid, size_t dyn_lds, hipStream_t stream) {
+  const qh_status st = allow_dyn_lds(&qmm_gemv_kernel<A16, FMT, LPBQ, MM>);
+  if (st != QH_STATUS_OK) return st;
+  hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MM>), grid, dim3(kGemvThreads), dyn_lds, stream, g);
+  const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "qmm_gemv_kernel launch");
   return QH_STATUS_OK;
 }
 
+template <bool A16, int FMT, bool LPBQ>
+qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
+  const int groups = g.N / 16;
+  // One group per workgroup while the staged activations are small; larger staging is
+  // amortised over several groups per workgroup.
+  const int planes = A16 ? 2 : 1;
+  int blocks = groups;
+  if (g.M > 4 && static_cast<size_t>(planes) * g.M * g.K > 16384 && blocks > 512) blocks = 512;
+  const dim3 grid(blocks);
+  if (g.M <= 1) return launch_one<A16, FMT, LPBQ, 1>(g, grid, dyn_lds, stream);
+  if (g.M <= 4) return launch_one<A16, FMT, LPBQ, 4>(g, grid, dyn_lds, stream);
+  return launch_one<A16, FMT, LPBQ, 16>(g, grid, dyn_lds, stream);
+}
+
+size_t align16(size_t x) { return (x + 15) & ~static_cast<size_t>(15); }
+
+// Dynamic LDS of one launch: activation planes, k-group sums, kFixBatch columns' weight words
+// and block scales (register-held fixup).
+struct GemvLds {
+  size_t off_asum, off_fixw, bytes;
+};
+GemvLds gemv_lds(const QmmShape &sh, int m) {
+  const int planes = sh.act_bits == 16 ? 2 : 1;
+  const int KG = sh.K / 32;
+  const int WB = sh.gemv_fmt == kTileI4 ? 16 : 32;
+  GemvLds L;
+  L.off_asum = align16(static_cast<size_t>(planes) * m * sh.K);
+  const size_t asum_bytes = sh.gemv_fmt == kTileI4 ? static_cast<size_t>(planes) * m * KG * 2 : 0;
+  L.off_fixw = align16(L.off_asum + asum_bytes);
+  // (only single-group launches, M <= 4, with one batch of k-groups hold the weights)
+  const bool reg_fix = m <= 4 && KG <= kGemvBatchKG;
+  L.bytes = L.off_fixw + (reg_fix ? static_cast<size_t>(kFixBatch) * KG * (WB + 1) : 0);
+  return L;
+}
+
 }  // namespace
+
+bool gemv_fits(const qh_qmm_prepared *p, int m) {
+  return m >= 1 && m <= 16 && gemv_lds(p->shape, m).bytes <= static_cast<size_t>(kGemvMaxDynLds);
+}
 
 qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream) {
   const QmmShape &sh = p->shape;
   const QmmDevice &D = p->dev;
-  const int planes = sh.act_bits == 16 ? 2 : 1;
   if (m > 16) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "GEMV path supports M <= 16 (got %d)", m);
-  if (static_cast<size_t>(planes) * m * sh.K > static_cast<size_t>(kGemvMaxLds))
-    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "GEMV path: M*K*planes = %zu bytes exceeds LDS staging (%d)",
-                static_cast<size_t>(planes) * m * sh.K, kGemvMaxLds);
+  const bool lpbq = sh.wfmt == QH_WEIGHT_I4_LPBQ;
+  const int KG = sh.K / 32;
+  const GemvLds L = gemv_lds(sh, m);
+  const size_t off_asum = L.off_asum, off_fixw = L.off_fixw, dyn = L.bytes;
+  if (dyn > static_cast<size_t>(kGemvMaxDynLds))
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "GEMV path: M=%d, K=%d needs %zu bytes of LDS staging (limit %d)", m,
+                sh.K, dyn, kGemvMaxDynLds);
   GemvArgs g{};
   g.act = static_cast<const uint8_t *>(act);
   g.out = out;
@@ -314,25 +573,26 @@ qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void
   g.M = m;
   g.N = sh.N;
   g.K = sh.K;
-  g.KG = sh.K / 32;
-  g.nblk = sh.lpbq_block ? sh.K / sh.lpbq_block : 0;
-  g.bs_shift = sh.lpbq_block == 64 ? 6 : 5;
+  g.KG = KG;
+  g.nbatch = (KG + kGemvBatchKG - 1) / kGemvBatchKG;
+  g.sub_shift = sh.lpbq_block == 64 ? 1 : 0;
   g.act_zp = sh.act_zp;
   g.out_zp = sh.out_zp;
   g.out_qmax = (1 << sh.out_bits) - 1;
   g.out16 = sh.out_bits == 16;
+  g.off_asum = static_cast<int>(off_asum);
+  g.off_fixw = static_cast<int>(off_fixw);
   g.sA = sh.act_scale;
   g.sO = sh.out_scale;
   const bool a16 = sh.act_bits == 16;
-  const bool lpbq = sh.wfmt == QH_WEIGHT_I4_LPBQ;
   if (!a16) {
-    if (sh.gemv_fmt == kTileI8) return launch_mm<false, kTileI8, false>(g, stream);
-    if (lpbq) return launch_mm<false, kTileI4, true>(g, stream);
-    return launch_mm<false, kTileI4, false>(g, stream);
+    if (sh.gemv_fmt == kTileI8) return launch_mm<false, kTileI8, false>(g, dyn, stream);
+    if (lpbq) return launch_mm<false, kTileI4, true>(g, dyn, stream);
+    return launch_mm<false, kTileI4, false>(g, dyn, stream);
   }
-  if (sh.gemv_fmt == kTileI8) return launch_mm<true, kTileI8, false>(g, stream);
-  if (lpbq) return launch_mm<true, kTileI4, true>(g, stream);
-  return launch_mm<true, kTileI4, false>(g, stream);
+  if (sh.gemv_fmt == kTileI8) return launch_mm<true, kTileI8, false>(g, dyn, stream);
+  if (lpbq) return launch_mm<true, kTileI4, true>(g, dyn, stream);
+  return launch_mm<true, kTileI4, false>(g, dyn, stream);
 }
 
 }  // namespace qh

@@ -42,6 +42,26 @@ __host__ __device__ inline int tile_off_i4(int c, int k) {
   return c * 64 + 8 * (((k & 127) >> 4) ^ swz_i4(c)) + (k & 7);  // nibble: (k & 8) ? high : low
 }
 
+// GEMV k-split: the 4 waves x 4 lanes of a workgroup that share a column take its 32-k groups
+// in batches of kGemvKU per lane; lane (wave w, sub s) takes kg = 16 i + 4 w + s in slot i of
+// the batch, so one batch covers kGemvBatchKG k-groups.
+constexpr int kGemvKU = 8;
+constexpr int kGemvBatchKG = 16 * kGemvKU;
+
+// LPBQ block scales of the GEMV stream, laid out so that a lane reads the kGemvKU scales of
+// its batch slots with one 8-byte load:
+//   [N/16 groups][batches][4 waves][4 >> sub_shift][16 columns][kGemvKU slots],
+// sub_shift = log2(block / 32): the lanes whose k-groups fall in one block share its scales.
+__host__ __device__ inline size_t gemv_scale_index(int grp, int batch, int nbatch, int wave, int subq, int nsubq,
+                                                   int col, int slot) {
+  return ((((static_cast<size_t>(grp) * nbatch + batch) * 4 + wave) * nsubq + subq) * 16 + col) * kGemvKU + slot;
+}
+__host__ __device__ inline size_t gemv_scale_index_kg(int n, int kg, int nbatch, int sub_shift) {
+  const int j = kg % kGemvBatchKG;
+  return gemv_scale_index(n / 16, kg / kGemvBatchKG, nbatch, (j >> 2) & 3, (j & 3) >> sub_shift, 4 >> sub_shift,
+                          n % 16, j >> 4);
+}
+
 // Everything the GEMM / GEMV kernels read, resident on the device.
 struct QmmDevice {
   // Weight operand tiles (GEMM).  For 16-bit activations the operand has 2N columns:
@@ -52,7 +72,7 @@ struct QmmDevice {
   // GEMV stream: per 256-column panel and 128-k tile, [256][64 B] nibbles (I4 / LPBQ) or
   // [256][128 B] int8 -- the same tile layout as the GEMM for 8-bit activations.
   uint8_t *gemv_tiles;
-  uint8_t *gemv_lpbq;   // [Np][Kp / lpbq_block] uint8 block scales for the GEMV stream
+  uint8_t *gemv_lpbq;   // LPBQ block scales for the GEMV stream (gemv_scale_index layout)
   // Per output channel epilogue constants.
   double *alpha;    // t = fma(S, alpha, beta): S is the exact integer dot product
   double *beta;     //   (alpha = sA * s32 / sO for 8-bit acts, sA * 2^E / sO for 16-bit)
@@ -104,6 +124,7 @@ qh_status hip_fail(hipError_t err, const char *what);
 // Kernel launchers (defined in the .hip files).
 qh_status launch_qmm_gemm(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
 qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
+bool gemv_fits(const qh_qmm_prepared *p, int m);  // the GEMV's LDS staging holds M x K
 qh_status launch_qmm_accumulate(const qh_qmm_prepared *p, int m, const void *act, int64_t *acc,
                                 hipStream_t stream);
 qh_status launch_gdn_solve_f32(const float *A, float *T, int heads, int C, int precision, hipStream_t stream);

@@ -259,11 +259,13 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
         }
       }
     if (lpbq) {
-      gemv_lpbq.assign(static_cast<size_t>(N) * nblk, 1);
+      const int nbatch = (KG + kGemvBatchKG - 1) / kGemvBatchKG;
+      const int sub_shift = bs == 64 ? 1 : 0;
+      gemv_lpbq.assign(static_cast<size_t>(N / 16) * nbatch * 4 * (4 >> sub_shift) * 16 * kGemvKU, 1);
       for (int n = 0; n < N; ++n)
-        for (int b = 0; b < nblk; ++b)
-          gemv_lpbq[(static_cast<size_t>(n / 16) * nblk + b) * 16 + (n % 16)] =
-              d->lpbq_block_scale[static_cast<size_t>(n) * nblk + b];
+        for (int kg = 0; kg < KG; ++kg)
+          gemv_lpbq[gemv_scale_index_kg(n, kg, nbatch, sub_shift)] =
+              d->lpbq_block_scale[static_cast<size_t>(n) * nblk + (kg * 32) / bs];
     }
   }
 
@@ -354,8 +356,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   // Bytes one GEMV call must stream: packed codes (+ block scales) of the logical N x K.
   {
     const uint64_t codes = static_cast<uint64_t>(N) * K / (sh.gemv_fmt == kTileI8 ? 1 : 2);
-    const uint64_t scales = lpbq ? static_cast<uint64_t>(N) * (K / bs) : 0;
-    p->gemv_weight_bytes = codes + scales;
+    p->gemv_weight_bytes = codes + gemv_lpbq.size();
   }
   *out = p;
   return QH_STATUS_OK;

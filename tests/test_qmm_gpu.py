@@ -104,7 +104,8 @@ def test_accumulators_exact(gpu, fam):
     op.close()
 
 
-SHAPES = [(1, 256, 32), (17, 96, 64), (300, 1024, 480), (257, 512, 288), (64, 4096, 256)]
+SHAPES = [(1, 256, 32), (17, 96, 64), (300, 1024, 480), (257, 512, 288), (64, 4096, 256), (1, 4128, 544),
+          (16, 4096, 96), (4, 8192, 64)]
 
 
 @pytest.mark.parametrize("fam", C.GATED_FAMILIES)
@@ -154,3 +155,19 @@ def test_near_tie_outputs_bit_exact(gpu, fam):
     print(f"[qmm] {fam} near-tie rows 0..15 gemv", flush=True)
     got = run(c, gpu, path=2, rows=16)
     assert np.array_equal(got, want[:16]), f"gemv: {diff_msg(got, want[:16])}"
+
+
+@pytest.mark.parametrize("fam", C.GATED_FAMILIES)
+@pytest.mark.parametrize("k", [512, 8192])
+@pytest.mark.parametrize("rows", [1, 4])
+def test_gemv_near_tie_decode_rows_bit_exact(gpu, fam, k, rows):
+    """Decode GEMV (1 and 4 rows) on tie / zero / rail rows: K = 512 recomputes uncertain
+    outputs from the weight words the workgroup holds in registers, K = 8192 (more than one
+    batch of k-groups per lane) re-reads them."""
+    from stress_cases import near_tie_case
+
+    c = near_tie_case(fam, 8, k, 96, 7, tie_rows=[0, 2], zero_rows=[3], rail_rows=[1])
+    want = oq.expected_output_case(c)[:rows]
+    print(f"[qmm] {fam} near-tie gemv rows={rows} k={k}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    assert np.array_equal(got, want), f"gemv: {diff_msg(got, want)}"
