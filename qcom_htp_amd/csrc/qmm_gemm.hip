@@ -1,8 +1,10 @@
 // Quantized GEMM on gfx950 i8 MFMA (v_mfma_i32_32x32x32_i8), bit-exact to the reference's
 // float-derived requantisation.
 //
-// Workgroup: 256 threads = 4 waves in a 2x2 grid over a 256 x 256 tile of the i8 operand
-// space (activation rows x weight-operand columns); each wave owns 4x4 MFMA 32x32 blocks.
+// Workgroup: 512 threads = 8 waves (two per SIMD) in a 2 x 4 grid over a 256 x 256 tile of
+// the i8 operand space (activation rows x weight-operand columns); each wave owns 4 x 2 MFMA
+// 32x32 blocks (128 rows x 64 columns).  Two waves per SIMD let one wave's LDS reads and
+// conversions run under the other's MFMAs (a lone wave stalls its MFMAs on its own LDS reads).
 // K is consumed 128 deep per pipeline step.
 //
 // Data movement: every operand tile goes global -> LDS with direct-to-LDS loads
@@ -63,6 +65,7 @@ struct GemmArgs {
 };
 
 constexpr int kTileA = 32768;  // A8: 256 rows x 128 B; A16: 128 rows x 256 B
+constexpr int kNT = 2;         // 32-column MFMA blocks per wave
 
 template <bool A16, int TFMT, bool LPBQ>
 struct Cfg {
@@ -70,8 +73,8 @@ struct Cfg {
   static constexpr int kTileF = LPBQ ? 1024 : 0;
   static constexpr int kStageBytes = kTileA + kTileB + kTileF;
   static constexpr int kStages = TFMT == kTileI8 ? 2 : 3;
-  static constexpr int kLoadsA = kTileA / 4096;   // 16-byte loads per thread per stage
-  static constexpr int kLoadsB = kTileB / 4096;
+  static constexpr int kLoadsA = kTileA / (16 * kGemmThreads);  // 16-byte loads per thread per stage
+  static constexpr int kLoadsB = kTileB / (16 * kGemmThreads);
   static constexpr int kLoads = kLoadsA + kLoadsB + (LPBQ ? 1 : 0);  // per wave per stage
   static constexpr int kArena = kStages * kStageBytes;
 };
@@ -293,7 +296,7 @@ __device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__
   using C = Cfg<A16, TFMT, LPBQ>;
 #pragma unroll
   for (int j = 0; j < C::kLoadsA; ++j) {
-    const int slot = j * 256 + c.t;  // 16-byte slot of the tile
+    const int slot = j * kGemmThreads + c.t;  // 16-byte slot of the tile
     const void *src;
     if (!A16) {
       const int row = slot >> 3, phys = slot & 7;
@@ -308,21 +311,23 @@ __device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__
       const int k = kt * kBK + 8 * logical < c.K ? kt * kBK + 8 * logical : c.K - 8;
       src = c.act + (static_cast<size_t>(m) * c.K + k) * 2;
     }
-    load_lds16(src, wa + (j * 256 + c.wave * 64) * 16);
+    load_lds16(src, wa + (j * kGemmThreads + c.wave * 64) * 16);
   }
   const uint8_t *bsrc = c.btiles + static_cast<size_t>(kt) * C::kTileB;
 #pragma unroll
-  for (int j = 0; j < C::kLoadsB; ++j) load_lds16(bsrc + (j * 256 + c.t) * 16, wb + (j * 256 + c.wave * 64) * 16);
+  for (int j = 0; j < C::kLoadsB; ++j)
+    load_lds16(bsrc + (j * kGemmThreads + c.t) * 16, wb + (j * kGemmThreads + c.wave * 64) * 16);
   if (LPBQ) {
     const uint8_t *fsrc = c.ftiles + static_cast<size_t>(kt) * C::kTileF;
-    if (c.lane < 16) load_lds16(fsrc + (c.wave * 16 + c.lane) * 16, wf + c.wave * 256);
+    // 1 KiB = 8 lanes x 16 B per wave (every wave issues the same number of loads)
+    if (c.lane < 8) load_lds16(fsrc + (c.wave * 8 + c.lane) * 16, wf + c.wave * 128);
   }
 }
 
 // Raw LDS words of one 32-k step: A fragments and B fragments (int4 tiles use .x/.y).
 struct RawStep {
   uint4 a[4];
-  uint4 b[4];
+  uint4 b[kNT];
 };
 
 template <bool A16, int TFMT>
@@ -341,8 +346,8 @@ __device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__res
       r.a[2 * mt + 1] = *reinterpret_cast<const uint4 *>(la + row * 256 + 16 * ((2 * s16 + 1) ^ swz16(row)));
     });
   }
-  static_for<4>([&](auto nt) {
-    const int col = c.wn * 128 + nt * 32 + (c.lane & 31);
+  static_for<kNT>([&](auto nt) {
+    const int col = c.wn * 64 + nt * 32 + (c.lane & 31);
     if (TFMT == kTileI8) {
       r.b[nt] = *reinterpret_cast<const uint4 *>(lb + col * 128 + 16 * (s16 ^ swz8(col)));
     } else {
@@ -360,7 +365,7 @@ __device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__res
 // Raw words -> MFMA operands: activations to signed bytes (16-bit: hi / lo' byte planes),
 // int4 weights widened (with the LPBQ block scale of the step).
 template <bool A16, int TFMT, bool LPBQ>
-__device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&fcol)[4], int kk, v4i (&af)[4], v4i (&bf)[4]) {
+__device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&fcol)[kNT], int kk, v4i (&af)[4], v4i (&bf)[kNT]) {
   if (!A16) {
     static_for<4>([&](auto mt) {
       const uint4 v = r.a[mt];
@@ -378,7 +383,7 @@ __device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&
                            static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
     });
   }
-  static_for<4>([&](auto nt) {
+  static_for<kNT>([&](auto nt) {
     const uint4 v = r.b[nt];
     if (TFMT == kTileI8) {
       bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
@@ -393,49 +398,95 @@ __device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&
   });
 }
 
-// One 128-k step on the tile held in (la, lb, lf), after issuing the loads of tile
-// kt + S - 1 into (wa, wb, wf).  The read and written stages are distinct LDS objects passed
-// as restrict pointers: the compiler may then let fragment reads run while the loads are in
-// flight (it would otherwise wait for every load before each read).  Fragment reads of the
-// next 32-k step are issued before the MFMAs of the current one.
-template <bool A16, int TFMT, bool LPBQ>
-__device__ __forceinline__ void k_step(const MainCtx &c, int kt, int KT, const uint8_t *__restrict__ la,
-                                       const uint8_t *__restrict__ lb, const uint8_t *__restrict__ lf,
-                                       uint8_t *__restrict__ wa, uint8_t *__restrict__ wb, uint8_t *__restrict__ wf,
-                                       v16i (&acc)[4][4]) {
-  using C = Cfg<A16, TFMT, LPBQ>;
-  constexpr int S = C::kStages;
-  // tile kt has landed once at most (S-2) later tiles are still in flight
-  if (S == 3 && kt + 1 < KT)
-    wait_vmcnt<(S - 2) * C::kLoads>();
+// The k loop is a software pipeline over 32-k steps sigma = 4 kt + kk (kt: 128-k tile, kk: its
+// 32-k step): step sigma runs its 16 MFMAs while the operands of step sigma + 1 are converted
+// (VALU) and the LDS fragments of step sigma + 2 are read, so the conversions issue in the
+// shadow of the matrix core rather than in bursts between MFMA groups (with one wave per SIMD
+// nothing else would hide them).  Tiles: every stage is filled up front; in step 2 of tile kt
+// each wave has read all of tile kt, waits until tile kt + 1 has landed, and one barrier then
+// publishes tile kt + 1 and frees the stage of tile kt, which receives tile kt + S at once.
+// The first two steps of tile kt + 1 are read (and the first converted) during steps 2 and 3
+// of tile kt.
+template <bool A16, int TFMT>
+struct PipeRegs {
+  RawStep raw[2];    // LDS words of the steps sigma + 1 / sigma + 2 (slot sigma & 1)
+  v4i af[2][4];      // converted operands of steps sigma / sigma + 1 (slot sigma & 1)
+  v4i bf[2][kNT];
+  uint32_t fcur[kNT];  // LPBQ block scales of the current tile's columns (one byte per 32-k step)
+  uint32_t fnext[kNT]; //   ... and of the next tile's
+};
+
+template <bool LPBQ>
+__device__ __forceinline__ void read_fcol(const MainCtx &c, const uint8_t *__restrict__ lf, uint32_t (&f)[kNT]) {
+  static_for<kNT>([&](auto nt) {
+    const int col = c.wn * 64 + nt * 32 + (c.lane & 31);
+    f[nt] = LPBQ ? *reinterpret_cast<const uint32_t *>(lf + col * 4) : 1u;
+  });
+}
+
+// Wait until at most n of this wave's tiles are still in flight.
+template <int LOADS>
+__device__ __forceinline__ void wait_tiles(int n) {
+  if (n >= 2)
+    wait_vmcnt<2 * LOADS>();
+  else if (n == 1)
+    wait_vmcnt<LOADS>();
   else
     wait_vmcnt<0>();
-  // Workgroup barrier without the release fence of __syncthreads: that fence would wait for
-  // every load in flight.  Each wave has waited for its own loads of tile kt above, and all of
-  // its reads of the stage refilled next were consumed before it arrives here.
-  asm volatile("s_barrier" ::: "memory");
-  uint32_t fcol[4] = {1u, 1u, 1u, 1u};
-  if (LPBQ) {
-    static_for<4>([&](auto nt) {
-      const int col = c.wn * 128 + nt * 32 + (c.lane & 31);
-      fcol[nt] = *reinterpret_cast<const uint32_t *>(lf + col * 4);
-    });
-  }
-  RawStep raw[2];
-  v4i af[4], bf[4];
-  read_step<A16, TFMT>(c, la, lb, 0, raw[0]);
-  if (kt + S - 1 < KT) issue_tile<A16, TFMT, LPBQ>(c, kt + S - 1, wa, wb, wf);
-  convert_step<A16, TFMT, LPBQ>(raw[0], fcol, 0, af, bf);
+}
+
+// Workgroup barrier that waits for this wave's LDS reads (not for its loads in flight, which
+// the release fence of __syncthreads would also wait for).
+__device__ __forceinline__ void lds_read_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One 128-k tile kt in stage (la, lb, lf); the next tile is in (na, nb, nf).  On entry af/bf
+// slot 0 hold the converted operands of step 0 and raw slot 1 the LDS words of step 1.
+template <bool A16, int TFMT, bool LPBQ>
+__device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t *__restrict__ la, uint8_t *__restrict__ lb,
+                                       uint8_t *__restrict__ lf, const uint8_t *__restrict__ na,
+                                       const uint8_t *__restrict__ nb, const uint8_t *__restrict__ nf,
+                                       PipeRegs<A16, TFMT> &p, v16i (&acc)[4][kNT]) {
+  using C = Cfg<A16, TFMT, LPBQ>;
+  constexpr int S = C::kStages;
   static_for<4>([&](auto kkc) {
     constexpr int kk = decltype(kkc)::value;
-    if (kk < 3) read_step<A16, TFMT>(c, la, lb, kk + 1, raw[(kk + 1) & 1]);
+    if (kk == 2) {
+      // Every tile slot issues (past the end it reloads tile KT - 1 into a stage nobody reads
+      // again), so exactly S - 1 tiles are in flight here: let all but tile kt + 1 remain.
+      // The issue is not behind a branch, so its loads interleave with the MFMAs below.
+      wait_tiles<C::kLoads>(S - 2);
+      lds_read_barrier();
+      issue_tile<A16, TFMT, LPBQ>(c, min(kt + S, KT - 1), la, lb, lf);
+      read_fcol<LPBQ>(c, nf, p.fnext);
+    }
+    // LDS words of step sigma + 2 (tile kt step kk + 2, or tile kt + 1 step kk - 2)
+    if (kk < 2)
+      read_step<A16, TFMT>(c, la, lb, kk + 2, p.raw[kk & 1]);
+    else
+      read_step<A16, TFMT>(c, na, nb, kk - 2, p.raw[kk & 1]);
+    // operands of step sigma + 1
+    if (kk < 3)
+      convert_step<A16, TFMT, LPBQ>(p.raw[(kk + 1) & 1], p.fcur, kk + 1, p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
+    else
+      convert_step<A16, TFMT, LPBQ>(p.raw[(kk + 1) & 1], p.fnext, 0, p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
+    // MFMAs of step sigma
     static_for<4>([&](auto mt) {
-      static_for<4>([&](auto nt) {
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[mt], bf[nt], acc[mt][nt], 0, 0, 0);
+      static_for<kNT>([&](auto nt) {
+        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(p.af[kk & 1][mt], p.bf[kk & 1][nt], acc[mt][nt], 0, 0, 0);
       });
     });
-    if (kk < 3) convert_step<A16, TFMT, LPBQ>(raw[(kk + 1) & 1], fcol, kk + 1, af, bf);
+    // issue order: the fragment reads early, then one MFMA and a few conversion instructions
+    // at a time
+    constexpr int kValu = TFMT == kTileI4 ? 6 : (A16 ? 3 : 2);  // conversion work per MFMA
+    static_for<4 * kNT>([&](auto i) {
+      constexpr int ii = decltype(i)::value;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if constexpr (ii < 4 + kNT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if constexpr (kk == 2 && ii < C::kLoads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, kValu + (kk == 2 ? 4 : 0), 0);
+    });
   });
+  static_for<kNT>([&](auto nt) { p.fcur[nt] = p.fnext[nt]; });
 }
 
 // MODE 0: requantised output; MODE 1: exact int64 accumulators sum_k (a - zp) * w_int.
@@ -459,7 +510,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   __shared__ double ctab[MODE == 0 ? 768 : 1];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn = wave >> 1;  // 128-row half, 64-column quarter of the tile
   int tm, tn;
   tile_of(blockIdx.x, g.TM, g.TN, &tm, &tn);
   const int rows_real = A16 ? kBM / 2 : kBM;
@@ -479,14 +530,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
 
   const MainCtx mc{act, btiles, ftiles, M, K, m0, t, lane, wave, wm, wn};
 
-  v16i acc[4][4];
-  static_for<4>([&](auto i) { static_for<4>([&](auto j) { acc[i][j] = v16i{}; }); });
+  v16i acc[4][kNT];
+  static_for<4>([&](auto i) { static_for<kNT>([&](auto j) { acc[i][j] = v16i{}; }); });
 
   // Per-column constants: loads issued ahead of the operand prologue, LDS writes after it (so
   // only these loads are waited for).
   double cv[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
   int64_t ccorr = 0, cmant = 0;
-  const int ccol = A16 ? (t & 127) : t;
+  const int ccol = A16 ? (t & 127) : (t & 255);
   const int cn = n0 + ccol < g.N ? n0 + ccol : 0;
   if (MODE == 0) {
     cv[0] = g.alpha[cn];
@@ -496,20 +547,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     ccorr = g.corr[cn];
     if (A16) cmant = g.mant[cn];
   }
-  static_for<S - 1>([&](auto p) {
-    if (p < KT) issue_tile<A16, TFMT, LPBQ>(mc, p, stage_a(p), stage_b(p), stage_f(p));
-  });
+  static_for<S>([&](auto p) { issue_tile<A16, TFMT, LPBQ>(mc, min(static_cast<int>(p), KT - 1), stage_a(p), stage_b(p), stage_f(p)); });
   if (MODE == 0) {
     const double alpha = cv[0];
     // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
     const double betap = fma(static_cast<double>(ccorr), alpha, cv[1]);
     const double corr_term = 2.0 * fabs(static_cast<double>(ccorr) * alpha);
-    if (!A16) {
+    if (!A16 && t < 256) {
       // |t - rint(t)| <= thr certifies the rounding; slack for |t| <= qmax + 2 folded in
       ctab[t] = alpha;
       ctab[256 + t] = betap;
       ctab[512 + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + static_cast<double>(g.out_qmax) + 2.0);
-    } else if (t < 128) {
+    } else if (A16 && t < 128) {
       // t = Y * alpha + (X * alpha M + beta'); |X| <= K * 33024 * 127 bounds the float slack
       const double alpha_m = alpha * static_cast<double>(cmant);
       const double umax = fabs(alpha_m) * static_cast<double>(K) * (33024.0 * 127.0);
@@ -521,15 +570,24 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   }
 
   // k loop, unrolled by the stage count so every stage is a compile-time LDS object
-  auto step = [&](const int kt, auto sc) __attribute__((always_inline)) {
-    constexpr int rs = decltype(sc)::value, ws = (rs + S - 1) % S;
-    k_step<A16, TFMT, LPBQ>(mc, kt, KT, stage_a(rs), stage_b(rs), stage_f(rs), stage_a(ws), stage_b(ws), stage_f(ws), acc);
+  PipeRegs<A16, TFMT> pr;
+  {
+    // tile 0 landed (the S - 1 later slots may stay in flight), its first steps read
+    wait_tiles<C::kLoads>(S - 1);
+    lds_read_barrier();  // also publishes the per-column constants written above
+    read_fcol<LPBQ>(mc, stage_f(std::integral_constant<int, 0>{}), pr.fcur);
+    read_step<A16, TFMT>(mc, stage_a(std::integral_constant<int, 0>{}), stage_b(std::integral_constant<int, 0>{}), 0, pr.raw[0]);
+    read_step<A16, TFMT>(mc, stage_a(std::integral_constant<int, 0>{}), stage_b(std::integral_constant<int, 0>{}), 1, pr.raw[1]);
+    convert_step<A16, TFMT, LPBQ>(pr.raw[0], pr.fcur, 0, pr.af[0], pr.bf[0]);
+  }
+  auto tile = [&](const int kt, auto sc) __attribute__((always_inline)) {
+    constexpr int rs = decltype(sc)::value, ns = (rs + 1) % S;
+    k_tile<A16, TFMT, LPBQ>(mc, kt, KT, stage_a(sc), stage_b(sc), stage_f(sc), stage_a(std::integral_constant<int, ns>{}),
+                            stage_b(std::integral_constant<int, ns>{}), stage_f(std::integral_constant<int, ns>{}), pr, acc);
   };
-  int kt0 = 0;
-  for (; kt0 + S <= KT; kt0 += S) static_for<S>([&](auto sc) { step(kt0 + sc, sc); });
-  static_for<S - 1>([&](auto sc) {
-    if (kt0 + sc < KT) step(kt0 + sc, sc);
-  });
+  for (int kt0 = 0; kt0 < KT; kt0 += S) static_for<S>([&](auto sc) {
+      if (kt0 + sc < KT) tile(kt0 + sc, sc);
+    });
   // ---------------------------------------------------------------- epilogue
   // Straight from the accumulator registers: each lane requantises the 4-row strips of its
   // MFMA blocks (one column), then the 4 lanes of a quad transpose their strips (DPP quad
@@ -543,14 +601,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // candidate roundings clamp to the same output).
   const int q = lane & 3;
   const double qmaxd = static_cast<double>(g.out_qmax);
-  constexpr int kBlocks = A16 ? 4 : 16;  // 32-row x 32-column blocks per lane
-  uint32_t *const flagw = reinterpret_cast<uint32_t *>(sA0);  // [kBlocks][256 threads]
+  constexpr int kBlocks = A16 ? 2 : 4 * kNT;  // 32-row x 32-column output blocks per lane
+  uint32_t *const flagw = reinterpret_cast<uint32_t *>(sA0);  // [kBlocks][kGemmThreads]
   uint8_t *const flagb = sA0;
   if (MODE == 1) {
     // exact int64 accumulators sum_k (a - zp) * w_int
     if (!A16) {
-      static_for<4>([&](auto nt) {
-        const int n = n0 + wn * 128 + nt * 32 + (lane & 31);
+      static_for<kNT>([&](auto nt) {
+        const int n = n0 + wn * 64 + nt * 32 + (lane & 31);
         if (n >= g.N) return;
         const int64_t corr = g.corr[n];
         static_for<4>([&](auto mt) {
@@ -563,8 +621,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
         });
       });
     } else {
-      static_for<2>([&](auto c) {
-        const int n = n0 + wn * 64 + c * 32 + (lane & 31);
+      {
+        // the wave's 64 operand columns: 32 weight-code columns, then their 32 residue columns
+        const int n = n0 + wn * 32 + (lane & 31);
         if (n >= g.N) return;
         const int64_t csum = g.colsum[n] * static_cast<int64_t>(128 + 32768 - g.act_zp);
         static_for<2>([&](auto mt) {
@@ -573,10 +632,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             const int m = m0 + wm * 64 + mt * 32 + 8 * (j / 4) + 4 * (lane >> 5) + (j % 4);
             if (m < M)
               reinterpret_cast<int64_t *>(g.out)[static_cast<size_t>(m) * g.N + n] =
-                  256 * static_cast<int64_t>(acc[2 * mt][2 * c][j]) + acc[2 * mt + 1][2 * c][j] + csum;
+                  256 * static_cast<int64_t>(acc[2 * mt][0][j]) + acc[2 * mt + 1][0][j] + csum;
           });
         });
-      });
+      }
     }
     return;
   }
@@ -587,8 +646,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   uint8_t *const tile_out = static_cast<uint8_t *>(g.out) + (static_cast<size_t>(m0) * g.N + n0) * esz;
   const bool full = m0 + rows_real <= M && n0 + cols_real <= g.N;
   if (!A16) {
-    static_for<4>([&](auto nt) {
-      const int cl = wn * 128 + nt * 32 + (lane & 31);  // column inside the tile
+    static_for<kNT>([&](auto nt) {
+      const int cl = wn * 64 + nt * 32 + (lane & 31);  // column inside the tile
       const double alpha = ctab[cl], beta = ctab[256 + cl], thr = ctab[512 + cl];
       static_for<4>([&](auto mt) {
         static_for<4>([&](auto jg) {
@@ -611,7 +670,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             });
             flagb[((nt * 4 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(fm);
           }
-          store_strip(g, tile_out, m0, n0, R + q, wn * 128 + nt * 32 + (lane & 28), o, q, full);
+          store_strip(g, tile_out, m0, n0, R + q, wn * 64 + nt * 32 + (lane & 28), o, q, full);
         });
       });
     });
@@ -619,8 +678,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     // 16-bit activations: real row tiles mt (32 rows), real column tiles c (32 columns);
     // acc[2mt + p][2c + s]: p = hi / lo' activation byte, s = weight code / rounding residue.
     // X = sum (a-32768)' q and Y = sum (a-32768)' r are exact in float64.
-    static_for<2>([&](auto c) {
-      const int cl = wn * 64 + c * 32 + (lane & 31);
+    {
+      constexpr int c = 0;  // one group of 32 real columns per wave
+      const int cl = wn * 32 + (lane & 31);
       const double alpha = ctab[cl], alpha_m = ctab[128 + cl], beta = ctab[256 + cl], thr = ctab[384 + cl];
       static_for<2>([&](auto mt) {
         static_for<4>([&](auto jg) {
@@ -647,10 +707,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             });
             flagb[((c * 2 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(fm);
           }
-          store_strip(g, tile_out, m0, n0, R + q, wn * 64 + c * 32 + (lane & 28), o, q, full);
+          store_strip(g, tile_out, m0, n0, R + q, wn * 32 + (lane & 28), o, q, full);
         });
       });
-    });
+    }
   }
 
   // ---------------------------------------------------------------- exact fixup
@@ -678,7 +738,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
       if (mk == 0) continue;
       uint32_t keep = 0;
       const int rb = A16 ? wm * 64 + (b & 1) * 32 + 4 * (lane >> 5) : wm * 128 + (b & 3) * 32 + 4 * (lane >> 5);
-      const int c = A16 ? wn * 64 + (b >> 1) * 32 + (lane & 31) : wn * 128 + (b >> 2) * 32 + (lane & 31);
+      const int c = A16 ? wn * 32 + (lane & 31) : wn * 64 + (b >> 2) * 32 + (lane & 31);
       while (mk) {
         const int bit = __builtin_ctz(mk);
         mk &= mk - 1;

@@ -13,7 +13,7 @@ namespace qh {
 constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kBK = 128;
-constexpr int kGemmThreads = 256;
+constexpr int kGemmThreads = 512;
 // Capacity of the per-workgroup list of outputs that need the exact fp64 fixup.
 constexpr int kFixCap = 1024;
 
