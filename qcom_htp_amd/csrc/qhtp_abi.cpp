@@ -108,7 +108,7 @@ qh_status qh_qmm_release(qh_qmm_prepared *prep) {
   (void)hipSetDevice(prep->device_id);
   hipError_t err = hipDeviceSynchronize();
   QmmDevice &D = prep->dev;
-  void *ptrs[] = {D.tiles, D.lpbq_tiles, D.gemv_tiles, D.gemv_lpbq, D.alpha, D.beta, D.corr,
+  void *ptrs[] = {D.tiles, D.gemv_tiles, D.gemv_lpbq, D.alpha, D.beta, D.corr,
                   D.margin, D.absb, D.bias_deq, D.s32, D.mant, D.colsum, D.gemv_margin_r1,
                   D.colsum_r, D.alpha_e, D.scale_exp, D.margin_exact};
   for (void *p : ptrs)

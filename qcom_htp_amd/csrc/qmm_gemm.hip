@@ -8,17 +8,15 @@
 // K is consumed 128 deep per pipeline step.
 //
 // Data movement: every operand tile goes global -> LDS with direct-to-LDS loads
-// (global_load_lds_dwordx4), bypassing VGPRs; STAGES tiles are in flight and one barrier per
-// step both publishes the landed tile and frees the oldest stage.  Weight tiles are prepared
-// as the exact LDS image (pre-swizzled), activation tiles are gathered into the swizzled
-// layout by the per-lane source addresses.  Operand conversion happens on the MFMA fragments
-// after the LDS read:
+// (global_load_lds_dwordx4), bypassing VGPRs; both stages are in flight and one barrier per
+// 128-k tile both publishes the landed tile and frees the stage read before.  Weight tiles are
+// int8 (int4 codes and LPBQ code * block scale are widened at prepare time) and prepared as
+// the exact LDS image (pre-swizzled); activation tiles are gathered into the swizzled layout
+// by the per-lane source addresses.  Activations are converted on the MFMA fragments after
+// the LDS read:
 //   * 8-bit activations: XOR 0x80 gives the signed a - 128;
 //   * 16-bit activations a - 32768 = 256*hi + lo' + 128: the hi and lo' bytes of each u16
-//     become two int8 fragments, each multiplied into its own accumulator;
-//   * int4 weights (offset-binary nibbles) widen to int8 in registers, LPBQ block scales are
-//     applied there too: (u*f + 128 - 8f) ^ 0x80 per byte is the two's complement of
-//     (u - 8) * f without carries between bytes.
+//     become two int8 fragments, each multiplied into its own accumulator.
 // Epilogue: straight from the accumulator registers.  The exact integer dot product S becomes
 // t = S*alpha + beta in float64; rint(t) is certain unless t is within the per-channel margin
 // of a rounding boundary, in which case the element is queued in LDS and recomputed after the
@@ -53,7 +51,6 @@ struct GemmArgs {
   const uint8_t *act;
   void *out;
   const uint8_t *tiles;
-  const uint8_t *lpbq;
   const double *alpha, *beta, *margin, *absb, *bias_deq;
   const double *alpha_e, *margin_exact;
   const int32_t *scale_exp;
@@ -67,16 +64,12 @@ struct GemmArgs {
 constexpr int kTileA = 32768;  // A8: 256 rows x 128 B; A16: 128 rows x 256 B
 constexpr int kNT = 2;         // 32-column MFMA blocks per wave
 
-template <bool A16, int TFMT, bool LPBQ>
 struct Cfg {
-  static constexpr int kTileB = TFMT == kTileI8 ? 32768 : 16384;
-  static constexpr int kTileF = LPBQ ? 1024 : 0;
-  static constexpr int kStageBytes = kTileA + kTileB + kTileF;
-  static constexpr int kStages = TFMT == kTileI8 ? 2 : 3;
+  static constexpr int kTileB = 32768;  // 256 operand columns x 128 k, int8
+  static constexpr int kStages = 2;
   static constexpr int kLoadsA = kTileA / (16 * kGemmThreads);  // 16-byte loads per thread per stage
   static constexpr int kLoadsB = kTileB / (16 * kGemmThreads);
-  static constexpr int kLoads = kLoadsA + kLoadsB + (LPBQ ? 1 : 0);  // per wave per stage
-  static constexpr int kArena = kStages * kStageBytes;
+  static constexpr int kLoads = kLoadsA + kLoadsB;  // per wave per stage
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -94,11 +87,6 @@ __device__ __forceinline__ void load_lds16(const void *gsrc, void *lds_wave_base
   __builtin_amdgcn_global_load_lds((gbl_void_ptr)(const_cast<void *>(gsrc)), (lds_void_ptr)(lds_wave_base), 16, 0, 0);
 }
 
-// int4 offset-binary nibbles (already masked to 0x0F per byte) -> int8 (u - 8) * f.
-__device__ __forceinline__ uint32_t widen4(uint32_t x, uint32_t f, uint32_t bias) {
-  return (x * f + bias) ^ 0x80808080u;
-}
-
 __device__ __forceinline__ void store_out(void *out, int out16, size_t idx, int v) {
   if (out16)
     static_cast<uint16_t *>(out)[idx] = static_cast<uint16_t>(v);
@@ -107,27 +95,12 @@ __device__ __forceinline__ void store_out(void *out, int out16, size_t idx, int 
 }
 
 // 16 consecutive integer weights (k .. k+15, k % 16 == 0) of operand column cb.
-template <int TFMT, bool LPBQ>
 __device__ __forceinline__ void load_w16(const GemmArgs g, int cb, int k, int (&w)[16]) {
   const size_t tile = static_cast<size_t>(cb / kBN) * g.KT + k / kBK;
-  if (TFMT == kTileI8) {
-    const uint8_t *p = g.tiles + tile * (kBN * kBK) + tile_off_i8(cb % kBN, k);
-    uint4 v = *reinterpret_cast<const uint4 *>(p);
-    const int8_t *b = reinterpret_cast<const int8_t *>(&v);
+  const uint4 v = *reinterpret_cast<const uint4 *>(g.tiles + tile * (kBN * kBK) + tile_off_i8(cb % kBN, k));
+  const int8_t *b = reinterpret_cast<const int8_t *>(&v);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) w[j] = b[j];
-  } else {
-    const uint8_t *p = g.tiles + tile * (kBN * kBK / 2) + tile_off_i4(cb % kBN, k);
-    uint2 v = *reinterpret_cast<const uint2 *>(p);
-    const uint8_t *b = reinterpret_cast<const uint8_t *>(&v);
-    int f = 1;
-    if (LPBQ) f = g.lpbq[tile * (kBN * 4) + (cb % kBN) * 4 + ((k & 127) >> 5)];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      w[j] = ((b[j] & 15) - 8) * f;
-      w[j + 8] = ((b[j] >> 4) - 8) * f;
-    }
-  }
+  for (int j = 0; j < 16; ++j) w[j] = b[j];
 }
 
 // Lane q of a quad holds outputs o[0..3] of tile rows R..R+3 in its own column; the quad
@@ -184,36 +157,16 @@ __device__ __forceinline__ double round_near(double t, double qmax, int *oi) {
   return fabs(tc - (y - kMagic));
 }
 
-// 16 consecutive weights of operand column cb, kept packed: I8 codes in v, or int4 nibbles in
-// v.x / v.y (byte j: k = j low nibble, k = j + 8 high nibble) with the LPBQ block scale f.
-struct WRaw {
-  uint4 v;
-  int f;
-};
-template <int TFMT, bool LPBQ>
-__device__ __forceinline__ WRaw load_w16_raw(const GemmArgs &g, int cb, int k) {
+// 16 consecutive int8 weights of operand column cb, kept packed.
+__device__ __forceinline__ uint4 load_w16_raw(const GemmArgs &g, int cb, int k) {
   const size_t tile = static_cast<size_t>(cb / kBN) * g.KT + k / kBK;
-  WRaw r;
-  r.f = 1;
-  if (TFMT == kTileI8) {
-    r.v = *reinterpret_cast<const uint4 *>(g.tiles + tile * (kBN * kBK) + tile_off_i8(cb % kBN, k));
-  } else {
-    const uint2 h = *reinterpret_cast<const uint2 *>(g.tiles + tile * (kBN * kBK / 2) + tile_off_i4(cb % kBN, k));
-    r.v = make_uint4(h.x, h.y, 0u, 0u);
-    if (LPBQ) r.f = g.lpbq[tile * (kBN * 4) + (cb % kBN) * 4 + ((k & 127) >> 5)];
-  }
-  return r;
+  return *reinterpret_cast<const uint4 *>(g.tiles + tile * (kBN * kBK) + tile_off_i8(cb % kBN, k));
 }
-template <int TFMT>
-__device__ __forceinline__ int w_at(const WRaw &r, int j) {
-  if (TFMT == kTileI8) return reinterpret_cast<const int8_t *>(&r.v)[j];
-  const int b = reinterpret_cast<const uint8_t *>(&r.v)[j & 7];
-  return ((j < 8 ? (b & 15) : (b >> 4)) - 8) * r.f;
-}
+__device__ __forceinline__ int w_at(const uint4 &v, int j) { return reinterpret_cast<const int8_t *>(&v)[j]; }
 
 // Exact float64 recomputation of one output, term by term as the oracle forms it:
 // sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), then + bias_deq, / sO, + out_zp, rint, clip.
-template <bool A16, int TFMT, bool LPBQ>
+template <bool A16>
 __device__ __forceinline__ void fixup_one(const GemmArgs &g, int m, int n, int lane) {
   const int cb = A16 ? (n / 32) * 64 + (n % 32) : n;
   const float sc = g.s32[n];
@@ -228,7 +181,7 @@ __device__ __forceinline__ void fixup_one(const GemmArgs &g, int m, int n, int l
       const int kc = kc0 + lane + 64 * i;
       if (kc < g.K / 16) {
         const int k = kc * 16;
-        load_w16<TFMT, LPBQ>(g, cb, k, w[i]);
+        load_w16(g, cb, k, w[i]);
         if (A16) {
           const uint4 *ap = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(g.act) + static_cast<size_t>(m) * g.K + k);
           av[i][0] = ap[0];
@@ -285,15 +238,13 @@ __device__ __forceinline__ void tile_of(int w, int TM, int TN, int *tm, int *tn)
 struct MainCtx {
   const uint8_t *act;     // activations [M][K] (u8) or [M][K] (u16)
   const uint8_t *btiles;  // weight tiles of this column panel, one per 128-k step
-  const uint8_t *ftiles;  // LPBQ block-scale tiles of this column panel
   int M, K, m0, t, lane, wave, wm, wn;
 };
 
-// Issue the direct-to-LDS loads of k-tile kt into the stage (wa, wb, wf).
-template <bool A16, int TFMT, bool LPBQ>
-__device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__restrict__ wa, uint8_t *__restrict__ wb,
-                                           uint8_t *__restrict__ wf) {
-  using C = Cfg<A16, TFMT, LPBQ>;
+// Issue the direct-to-LDS loads of k-tile kt into the stage (wa, wb).
+template <bool A16>
+__device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__restrict__ wa, uint8_t *__restrict__ wb) {
+  using C = Cfg;
 #pragma unroll
   for (int j = 0; j < C::kLoadsA; ++j) {
     const int slot = j * kGemmThreads + c.t;  // 16-byte slot of the tile
@@ -317,20 +268,15 @@ __device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__
 #pragma unroll
   for (int j = 0; j < C::kLoadsB; ++j)
     load_lds16(bsrc + (j * kGemmThreads + c.t) * 16, wb + (j * kGemmThreads + c.wave * 64) * 16);
-  if (LPBQ) {
-    const uint8_t *fsrc = c.ftiles + static_cast<size_t>(kt) * C::kTileF;
-    // 1 KiB = 8 lanes x 16 B per wave (every wave issues the same number of loads)
-    if (c.lane < 8) load_lds16(fsrc + (c.wave * 8 + c.lane) * 16, wf + c.wave * 128);
-  }
 }
 
-// Raw LDS words of one 32-k step: A fragments and B fragments (int4 tiles use .x/.y).
+// Raw LDS words of one 32-k step: A fragments and B fragments.
 struct RawStep {
   uint4 a[4];
   uint4 b[kNT];
 };
 
-template <bool A16, int TFMT>
+template <bool A16>
 __device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__restrict__ la, const uint8_t *__restrict__ lb,
                                           int kk, RawStep &r) {
   const int s16 = 2 * kk + (c.lane >> 5);  // 16-k chunk index inside the 128-k tile
@@ -348,24 +294,14 @@ __device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__res
   }
   static_for<kNT>([&](auto nt) {
     const int col = c.wn * 64 + nt * 32 + (c.lane & 31);
-    if (TFMT == kTileI8) {
-      r.b[nt] = *reinterpret_cast<const uint4 *>(lb + col * 128 + 16 * (s16 ^ swz8(col)));
-    } else {
-      // the offset is hidden from the compiler so that it does not merge the four 8-byte reads
-      // into ds_read2 pairs (the merged reads lose the no-alias information and would wait
-      // for the loads in flight)
-      int off = col * 64 + 8 * (s16 ^ swz_i4(col));
-      asm volatile("" : "+v"(off));
-      const uint2 v = *reinterpret_cast<const uint2 *>(lb + off);
-      r.b[nt] = make_uint4(v.x, v.y, 0u, 0u);
-    }
+    r.b[nt] = *reinterpret_cast<const uint4 *>(lb + col * 128 + 16 * (s16 ^ swz8(col)));
   });
 }
 
-// Raw words -> MFMA operands: activations to signed bytes (16-bit: hi / lo' byte planes),
-// int4 weights widened (with the LPBQ block scale of the step).
-template <bool A16, int TFMT, bool LPBQ>
-__device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&fcol)[kNT], int kk, v4i (&af)[4], v4i (&bf)[kNT]) {
+// Raw words -> MFMA operands: activations to signed bytes (16-bit: hi / lo' byte planes); the
+// int8 weight words are used as they are.
+template <bool A16>
+__device__ __forceinline__ void convert_step(const RawStep &r, v4i (&af)[4], v4i (&bf)[kNT]) {
   if (!A16) {
     static_for<4>([&](auto mt) {
       const uint4 v = r.a[mt];
@@ -385,44 +321,23 @@ __device__ __forceinline__ void convert_step(const RawStep &r, const uint32_t (&
   }
   static_for<kNT>([&](auto nt) {
     const uint4 v = r.b[nt];
-    if (TFMT == kTileI8) {
-      bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-    } else {
-      uint32_t f = 1;
-      if (LPBQ) f = (fcol[nt] >> (8 * kk)) & 0xFFu;
-      const uint32_t bias = (128u - 8u * f) * 0x01010101u;
-      const uint32_t m4 = 0x0F0F0F0Fu;
-      bf[nt] = v4i{static_cast<int>(widen4(v.x & m4, f, bias)), static_cast<int>(widen4(v.y & m4, f, bias)),
-                   static_cast<int>(widen4((v.x >> 4) & m4, f, bias)), static_cast<int>(widen4((v.y >> 4) & m4, f, bias))};
-    }
+    bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
   });
 }
 
 // The k loop is a software pipeline over 32-k steps sigma = 4 kt + kk (kt: 128-k tile, kk: its
-// 32-k step): step sigma runs its 16 MFMAs while the operands of step sigma + 1 are converted
+// 32-k step): step sigma runs its MFMAs while the operands of step sigma + 1 are converted
 // (VALU) and the LDS fragments of step sigma + 2 are read, so the conversions issue in the
-// shadow of the matrix core rather than in bursts between MFMA groups (with one wave per SIMD
-// nothing else would hide them).  Tiles: every stage is filled up front; in step 2 of tile kt
-// each wave has read all of tile kt, waits until tile kt + 1 has landed, and one barrier then
-// publishes tile kt + 1 and frees the stage of tile kt, which receives tile kt + S at once.
-// The first two steps of tile kt + 1 are read (and the first converted) during steps 2 and 3
-// of tile kt.
-template <bool A16, int TFMT>
+// shadow of the matrix core rather than in bursts between MFMA groups.  Tiles: both stages
+// are filled up front; in step 2 of tile kt each wave has read all of tile kt, waits until
+// tile kt + 1 has landed, and one barrier then publishes tile kt + 1 and frees the stage of
+// tile kt, which receives tile kt + 2 at once.  The first two steps of tile kt + 1 are read
+// (and the first converted) during steps 2 and 3 of tile kt.
 struct PipeRegs {
   RawStep raw[2];    // LDS words of the steps sigma + 1 / sigma + 2 (slot sigma & 1)
   v4i af[2][4];      // converted operands of steps sigma / sigma + 1 (slot sigma & 1)
   v4i bf[2][kNT];
-  uint32_t fcur[kNT];  // LPBQ block scales of the current tile's columns (one byte per 32-k step)
-  uint32_t fnext[kNT]; //   ... and of the next tile's
 };
-
-template <bool LPBQ>
-__device__ __forceinline__ void read_fcol(const MainCtx &c, const uint8_t *__restrict__ lf, uint32_t (&f)[kNT]) {
-  static_for<kNT>([&](auto nt) {
-    const int col = c.wn * 64 + nt * 32 + (c.lane & 31);
-    f[nt] = LPBQ ? *reinterpret_cast<const uint32_t *>(lf + col * 4) : 1u;
-  });
-}
 
 // Wait until at most n of this wave's tiles are still in flight.
 template <int LOADS>
@@ -439,14 +354,13 @@ __device__ __forceinline__ void wait_tiles(int n) {
 // the release fence of __syncthreads would also wait for).
 __device__ __forceinline__ void lds_read_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// One 128-k tile kt in stage (la, lb, lf); the next tile is in (na, nb, nf).  On entry af/bf
-// slot 0 hold the converted operands of step 0 and raw slot 1 the LDS words of step 1.
-template <bool A16, int TFMT, bool LPBQ>
+// One 128-k tile kt in stage (la, lb); the next tile is in (na, nb).  On entry af/bf slot 0
+// hold the converted operands of step 0 and raw slot 1 the LDS words of step 1.
+template <bool A16>
 __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t *__restrict__ la, uint8_t *__restrict__ lb,
-                                       uint8_t *__restrict__ lf, const uint8_t *__restrict__ na,
-                                       const uint8_t *__restrict__ nb, const uint8_t *__restrict__ nf,
-                                       PipeRegs<A16, TFMT> &p, v16i (&acc)[4][kNT]) {
-  using C = Cfg<A16, TFMT, LPBQ>;
+                                       const uint8_t *__restrict__ na, const uint8_t *__restrict__ nb, PipeRegs &p,
+                                       v16i (&acc)[4][kNT]) {
+  using C = Cfg;
   constexpr int S = C::kStages;
   static_for<4>([&](auto kkc) {
     constexpr int kk = decltype(kkc)::value;
@@ -456,19 +370,15 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
       // The issue is not behind a branch, so its loads interleave with the MFMAs below.
       wait_tiles<C::kLoads>(S - 2);
       lds_read_barrier();
-      issue_tile<A16, TFMT, LPBQ>(c, min(kt + S, KT - 1), la, lb, lf);
-      read_fcol<LPBQ>(c, nf, p.fnext);
+      issue_tile<A16>(c, min(kt + S, KT - 1), la, lb);
     }
     // LDS words of step sigma + 2 (tile kt step kk + 2, or tile kt + 1 step kk - 2)
     if (kk < 2)
-      read_step<A16, TFMT>(c, la, lb, kk + 2, p.raw[kk & 1]);
+      read_step<A16>(c, la, lb, kk + 2, p.raw[kk & 1]);
     else
-      read_step<A16, TFMT>(c, na, nb, kk - 2, p.raw[kk & 1]);
+      read_step<A16>(c, na, nb, kk - 2, p.raw[kk & 1]);
     // operands of step sigma + 1
-    if (kk < 3)
-      convert_step<A16, TFMT, LPBQ>(p.raw[(kk + 1) & 1], p.fcur, kk + 1, p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
-    else
-      convert_step<A16, TFMT, LPBQ>(p.raw[(kk + 1) & 1], p.fnext, 0, p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
+    convert_step<A16>(p.raw[(kk + 1) & 1], p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
     // MFMAs of step sigma
     static_for<4>([&](auto mt) {
       static_for<kNT>([&](auto nt) {
@@ -477,7 +387,7 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
     });
     // issue order: the fragment reads early, then one MFMA and a few conversion instructions
     // at a time
-    constexpr int kValu = TFMT == kTileI4 ? 6 : (A16 ? 3 : 2);  // conversion work per MFMA
+    constexpr int kValu = A16 ? 3 : 2;  // conversion work per MFMA
     static_for<4 * kNT>([&](auto i) {
       constexpr int ii = decltype(i)::value;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -486,22 +396,20 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
       __builtin_amdgcn_sched_group_barrier(0x002, kValu + (kk == 2 ? 4 : 0), 0);
     });
   });
-  static_for<kNT>([&](auto nt) { p.fcur[nt] = p.fnext[nt]; });
 }
 
 // MODE 0: requantised output; MODE 1: exact int64 accumulators sum_k (a - zp) * w_int.
 // CLAMP: clamp t before rounding (some column cannot prove |t| < 2^30).
-template <bool A16, int TFMT, bool LPBQ, int MODE, bool CLAMP>
+template <bool A16, int MODE, bool CLAMP>
 __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArgs g) {
-  using C = Cfg<A16, TFMT, LPBQ>;
+  using C = Cfg;
   // One LDS object per pipeline stage and operand: the compiler then knows that the
   // direct-to-LDS loads in flight (into other stages) cannot alias the fragment reads, and
   // does not make the reads wait for them.
   constexpr int S = C::kStages;
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[kTileA], sA1[kTileA], sA2[S > 2 ? kTileA : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t sB0[C::kTileB], sB1[C::kTileB], sB2[S > 2 ? C::kTileB : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t sF0[LPBQ ? C::kTileF : 16], sF1[LPBQ ? C::kTileF : 16],
-      sF2[LPBQ && S > 2 ? C::kTileF : 16];
+  static_assert(S == 2, "two stages");
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kTileA], sA1[kTileA];
+  __shared__ __attribute__((aligned(16))) uint8_t sB0[C::kTileB], sB1[C::kTileB];
   __shared__ uint32_t fix_list[kFixCap];  // (row << 16 | column) inside the tile
   __shared__ int fix_cnt;
   // Per-column epilogue constants of the tile, filled while the first operand tiles load.
@@ -520,15 +428,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const int M = g.M, K = g.K, KT = g.KT;
   const uint8_t *const act = g.act;
   const uint8_t *const btiles = g.tiles + static_cast<size_t>(tn) * KT * C::kTileB;
-  const uint8_t *const ftiles = LPBQ ? g.lpbq + static_cast<size_t>(tn) * KT * C::kTileF : nullptr;
   if (t == 0) fix_cnt = 0;
 
   // stage indices are compile-time constants everywhere (the k loop is unrolled by S)
-  auto stage_a = [&](auto st) -> uint8_t * { return st == 0 ? sA0 : (st == 1 ? sA1 : sA2); };
-  auto stage_b = [&](auto st) -> uint8_t * { return st == 0 ? sB0 : (st == 1 ? sB1 : sB2); };
-  auto stage_f = [&](auto st) -> uint8_t * { return st == 0 ? sF0 : (st == 1 ? sF1 : sF2); };
+  auto stage_a = [&](auto st) -> uint8_t * { return st == 0 ? sA0 : sA1; };
+  auto stage_b = [&](auto st) -> uint8_t * { return st == 0 ? sB0 : sB1; };
 
-  const MainCtx mc{act, btiles, ftiles, M, K, m0, t, lane, wave, wm, wn};
+  const MainCtx mc{act, btiles, M, K, m0, t, lane, wave, wm, wn};
 
   v16i acc[4][kNT];
   static_for<4>([&](auto i) { static_for<kNT>([&](auto j) { acc[i][j] = v16i{}; }); });
@@ -547,7 +453,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     ccorr = g.corr[cn];
     if (A16) cmant = g.mant[cn];
   }
-  static_for<S>([&](auto p) { issue_tile<A16, TFMT, LPBQ>(mc, min(static_cast<int>(p), KT - 1), stage_a(p), stage_b(p), stage_f(p)); });
+  static_for<S>([&](auto p) { issue_tile<A16>(mc, min(static_cast<int>(p), KT - 1), stage_a(p), stage_b(p)); });
   if (MODE == 0) {
     const double alpha = cv[0];
     // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
@@ -570,20 +476,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   }
 
   // k loop, unrolled by the stage count so every stage is a compile-time LDS object
-  PipeRegs<A16, TFMT> pr;
+  PipeRegs pr;
   {
     // tile 0 landed (the S - 1 later slots may stay in flight), its first steps read
     wait_tiles<C::kLoads>(S - 1);
     lds_read_barrier();  // also publishes the per-column constants written above
-    read_fcol<LPBQ>(mc, stage_f(std::integral_constant<int, 0>{}), pr.fcur);
-    read_step<A16, TFMT>(mc, stage_a(std::integral_constant<int, 0>{}), stage_b(std::integral_constant<int, 0>{}), 0, pr.raw[0]);
-    read_step<A16, TFMT>(mc, stage_a(std::integral_constant<int, 0>{}), stage_b(std::integral_constant<int, 0>{}), 1, pr.raw[1]);
-    convert_step<A16, TFMT, LPBQ>(pr.raw[0], pr.fcur, 0, pr.af[0], pr.bf[0]);
+    read_step<A16>(mc, sA0, sB0, 0, pr.raw[0]);
+    read_step<A16>(mc, sA0, sB0, 1, pr.raw[1]);
+    convert_step<A16>(pr.raw[0], pr.af[0], pr.bf[0]);
   }
   auto tile = [&](const int kt, auto sc) __attribute__((always_inline)) {
     constexpr int rs = decltype(sc)::value, ns = (rs + 1) % S;
-    k_tile<A16, TFMT, LPBQ>(mc, kt, KT, stage_a(sc), stage_b(sc), stage_f(sc), stage_a(std::integral_constant<int, ns>{}),
-                            stage_b(std::integral_constant<int, ns>{}), stage_f(std::integral_constant<int, ns>{}), pr, acc);
+    k_tile<A16>(mc, kt, KT, stage_a(sc), stage_b(sc), stage_a(std::integral_constant<int, ns>{}),
+                stage_b(std::integral_constant<int, ns>{}), pr, acc);
   };
   for (int kt0 = 0; kt0 < KT; kt0 += S) static_for<S>([&](auto sc) {
       if (kt0 + sc < KT) tile(kt0 + sc, sc);
@@ -782,7 +687,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
 #pragma unroll
       for (int i = 0; i < EW; ++i) S1[i] = S2[i] = 0;
       for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
-        WRaw wr[EW][P];
+        uint4 wr[EW][P];
         uint4 av[EW][P][A16 ? 2 : 1];
 #pragma unroll
         for (int i = 0; i < EW; ++i) {
@@ -791,7 +696,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             const int kc = kc0 + lane + 64 * pp;
             const int k = kc < KC ? kc * 16 : 0;
             const int n = ncol[i];
-            wr[i][pp] = load_w16_raw<TFMT, LPBQ>(g, A16 ? (n / 32) * 64 + (n % 32) : n, k);
+            wr[i][pp] = load_w16_raw(g, A16 ? (n / 32) * 64 + (n % 32) : n, k);
             const uint4 *ap = reinterpret_cast<const uint4 *>(act + (static_cast<size_t>(mrow[i]) * K + k) * (A16 ? 2 : 1));
             av[i][pp][0] = ap[0];
             if (A16) av[i][pp][A16 ? 1 : 0] = ap[1];
@@ -807,7 +712,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             for (int j = 0; j < 16; ++j) {
               const int a = (A16 ? static_cast<int>(reinterpret_cast<const uint16_t *>(&av[i][pp][j >> 3])[j & 7])
                                  : static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i][pp][0])[j])) - abase;
-              const int wj = w_at<TFMT>(wr[i][pp], j);
+              const int wj = w_at(wr[i][pp], j);
               // W' = fl32(w * s32) / 2^E = fl32(w * M) (s32 = M * 2^E, no subnormals): the
               // residue r = W' - w * M is minus the exact rounding error of that product
               const float wf = static_cast<float>(wj);
@@ -840,7 +745,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
         const double rd = rint(tv);
         const double slack = mx[i] + 0x1p-48 * (fabs(u) + fabs(tv) + ab[i]);
         if (fabs(tv - rd) > 0.5 - slack) {
-          fixup_one<A16, TFMT, LPBQ>(g, m, n, lane);
+          fixup_one<A16>(g, m, n, lane);
         } else if (lane == 0) {
           const int oi = static_cast<int>(rd);
           store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
@@ -853,13 +758,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   }
 }
 
-template <bool A16, int TFMT, bool LPBQ, int MODE>
+template <bool A16, int MODE>
 qh_status launch(const GemmArgs &g, bool clamp, hipStream_t stream) {
   dim3 grid(g.TM * g.TN);
   if (MODE == 0 && clamp)
-    hipLaunchKernelGGL((qmm_gemm_kernel<A16, TFMT, LPBQ, MODE, true>), grid, dim3(kGemmThreads), 0, stream, g);
+    hipLaunchKernelGGL((qmm_gemm_kernel<A16, MODE, true>), grid, dim3(kGemmThreads), 0, stream, g);
   else
-    hipLaunchKernelGGL((qmm_gemm_kernel<A16, TFMT, LPBQ, MODE, false>), grid, dim3(kGemmThreads), 0, stream, g);
+    hipLaunchKernelGGL((qmm_gemm_kernel<A16, MODE, false>), grid, dim3(kGemmThreads), 0, stream, g);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "qmm_gemm_kernel launch");
   return QH_STATUS_OK;
@@ -873,7 +778,6 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.act = static_cast<const uint8_t *>(act);
   g.out = out;
   g.tiles = D.tiles;
-  g.lpbq = D.lpbq_tiles;
   g.alpha = D.alpha;
   g.beta = D.beta;
   g.margin = D.margin;
@@ -902,15 +806,9 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.TN = sh.ncols_op / kBN;
   g.TM = (m + rows_real - 1) / rows_real;
   if (static_cast<long long>(g.TM) * g.TN > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "M=%d too large", m);
-  const bool lpbq_regs = sh.wfmt == QH_WEIGHT_I4_LPBQ && !a16;
   const bool clamp = sh.epi_clamp != 0;
-  if (!a16) {
-    if (sh.tile_fmt == kTileI8) return launch<false, kTileI8, false, MODE>(g, clamp, stream);
-    if (lpbq_regs) return launch<false, kTileI4, true, MODE>(g, clamp, stream);
-    return launch<false, kTileI4, false, MODE>(g, clamp, stream);
-  }
-  if (sh.tile_fmt == kTileI8) return launch<true, kTileI8, false, MODE>(g, clamp, stream);
-  return launch<true, kTileI4, false, MODE>(g, clamp, stream);
+  if (!a16) return launch<false, MODE>(g, clamp, stream);
+  return launch<true, MODE>(g, clamp, stream);
 }
 
 }  // namespace

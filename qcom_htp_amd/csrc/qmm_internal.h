@@ -17,29 +17,22 @@ constexpr int kGemmThreads = 512;
 // Capacity of the per-workgroup list of outputs that need the exact fp64 fixup.
 constexpr int kFixCap = 1024;
 
-// Tile storage of the weight operand (the "B" operand of the MFMA).  A tile (nt, kt) covers
-// 256 operand columns x 128 k and is stored exactly as the GEMM keeps it in LDS, so the kernel
-// fills LDS with straight 16-byte direct-to-LDS copies:
-//   kTileI8 : 32 KiB; column c owns 128 B = eight 16-k chunks, chunk s at 16 * (s ^ swz8(c)).
-//   kTileI4 : 16 KiB; two int4 codes per byte, offset-binary (code + 8); column c owns 64 B =
-//             eight 16-k groups of 8 B, group s at 8 * (s ^ swz_i4(c)); inside a group byte j
-//             holds k = j in its low nibble and k = j + 8 in its high nibble.
-// LPBQ block scales for the GEMM: per tile [256 cols][4] bytes, entry j = the scale of the
-// 32-k chunk j of the tile (1 KiB per tile, also an LDS image).
+// Tile storage of the GEMM weight operand (the "B" operand of the MFMA): int8 integer weights
+// (int4 codes and LPBQ code * block scale widened at prepare time).  A tile (nt, kt) covers 256
+// operand columns x 128 k (32 KiB) and is stored exactly as the GEMM keeps it in LDS, so the
+// kernel fills LDS with straight 16-byte direct-to-LDS copies: column c owns 128 B = eight 16-k
+// chunks, chunk s at 16 * (s ^ swz8(c)).
+// Element format of the decode GEMV stream: int8 codes, or int4 codes (two per byte).
 enum TileFormat : int { kTileI8 = 0, kTileI4 = 1 };
 
 // XOR swizzles that make the MFMA fragment reads bank-conflict free (32 consecutive rows or
 // columns reading the same logical chunk hit distinct banks for 8- or 16-lane LDS phases).
 __host__ __device__ inline int swz8(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
-__host__ __device__ inline int swz_i4(int col) { return (col >> 2) & 7; }
 __host__ __device__ inline int swz16(int row) { return row & 15; }
 
 // Byte offset of (operand column c, depth k) inside its tile.
 __host__ __device__ inline int tile_off_i8(int c, int k) {
   return c * 128 + 16 * (((k & 127) >> 4) ^ swz8(c)) + (k & 15);
-}
-__host__ __device__ inline int tile_off_i4(int c, int k) {
-  return c * 64 + 8 * (((k & 127) >> 4) ^ swz_i4(c)) + (k & 7);  // nibble: (k & 8) ? high : low
 }
 
 // GEMV k-split: the 4 waves x 4 lanes of a workgroup that share a column take its 32-k groups
@@ -68,9 +61,8 @@ struct QmmDevice {
   // inside each 64-column group, columns [0,32) carry the weight codes of 32 output
   // channels and columns [32,64) the fl32 rounding residues of the same channels.
   uint8_t *tiles;
-  uint8_t *lpbq_tiles;  // [Ncols_padded][Kp / lpbq_block] uint8 block scales (I4 LPBQ GEMM)
-  // GEMV stream: per 256-column panel and 128-k tile, [256][64 B] nibbles (I4 / LPBQ) or
-  // [256][128 B] int8 -- the same tile layout as the GEMM for 8-bit activations.
+  // GEMV stream: [N/16 column groups][K/32 k-groups][16 columns][16 B int4 | 32 B int8]
+  // (int4 byte j: k = j in the low nibble, k = j + 16 in the high nibble, offset-binary).
   uint8_t *gemv_tiles;
   uint8_t *gemv_lpbq;   // LPBQ block scales for the GEMV stream (gemv_scale_index layout)
   // Per output channel epilogue constants.
@@ -97,7 +89,6 @@ struct QmmShape {
   int ncols_op;       // columns of the weight operand (N or 2N), padded to kBN
   int act_bits, out_bits;
   int wfmt;           // qh_weight_format
-  int tile_fmt;       // TileFormat of the GEMM tiles
   int gemv_fmt;       // TileFormat of the GEMV stream
   int lpbq_block;     // 0 unless LPBQ
   int act_zp, out_zp;

@@ -67,28 +67,14 @@ struct DevAlloc {
 };
 
 // Writes value v (int8 range) of operand column c, depth k into the tile image.
+// Writes int8 weights into the GEMM tile layout (see qmm_internal.h).
 struct TileWriter {
   std::vector<uint8_t> &buf;
-  int fmt;
   int KT;  // number of 128-deep k tiles
   void put(int c, int k, int v) {
-    size_t tile = static_cast<size_t>(c / kBN) * KT + k / kBK;
-    int cc = c % kBN;
-    if (fmt == kTileI8) {
-      buf[tile * (kBN * kBK) + tile_off_i8(cc, k)] = static_cast<uint8_t>(static_cast<int8_t>(v));
-    } else {
-      size_t off = tile * (kBN * kBK / 2) + tile_off_i4(cc, k);
-      uint8_t nib = static_cast<uint8_t>((v + 8) & 15);
-      if ((k & 8) == 0)
-        buf[off] = static_cast<uint8_t>((buf[off] & 0xF0) | nib);
-      else
-        buf[off] = static_cast<uint8_t>((buf[off] & 0x0F) | (nib << 4));
-    }
+    const size_t tile = static_cast<size_t>(c / kBN) * KT + k / kBK;
+    buf[tile * (kBN * kBK) + tile_off_i8(c % kBN, k)] = static_cast<uint8_t>(static_cast<int8_t>(v));
   }
-  static size_t bytes_for(int fmt, int ncols, int Kp) {
-    return static_cast<size_t>(ncols) * Kp / (fmt == kTileI8 ? 1 : 2);
-  }
-  static uint8_t zero_byte(int fmt) { return fmt == kTileI8 ? 0x00 : 0x88; }
 };
 
 }  // namespace
@@ -193,15 +179,15 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   sh.act_scale = d->act_scale;
   sh.out_scale = d->out_scale;
   const bool a16 = d->act_bits == 16;
-  bool resid_fits_nibble = true;
-  for (size_t i = 0; i < resid.size() && resid_fits_nibble; ++i) resid_fits_nibble = resid[i] >= -8 && resid[i] <= 7;
+  // The GEMM is bound by the matrix cores, not by its weight bytes: int4 codes (and LPBQ
+  // code * block scale, |.| <= 112) are widened to int8 tiles here, once, which keeps every
+  // conversion but the activation shift out of its main loop.  The decode GEMV, which is bound
+  // by HBM, streams the int4 codes.
   if (!a16) {
-    sh.tile_fmt = d->weight_format == QH_WEIGHT_I8 ? kTileI8 : kTileI4;
     sh.ncols_op = round_up(N, kBN);
     sh.Np = sh.ncols_op;
   } else {
-    // codes and residues share one operand; nibbles only when both fit.
-    sh.tile_fmt = (d->weight_format == QH_WEIGHT_I4 && resid_fits_nibble) ? kTileI4 : kTileI8;
+    // codes and residues share one operand
     sh.ncols_op = round_up(2 * N, kBN);
     sh.Np = sh.ncols_op / 2;
   }
@@ -209,26 +195,11 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   const int KT = sh.Kp / kBK;
 
   // ---- GEMM operand tiles ------------------------------------------------------------------
-  std::vector<uint8_t> tiles(TileWriter::bytes_for(sh.tile_fmt, sh.ncols_op, sh.Kp), TileWriter::zero_byte(sh.tile_fmt));
-  TileWriter tw{tiles, sh.tile_fmt, KT};
-  std::vector<uint8_t> lpbq_tiles;
-  const bool gemm_lpbq_regs = lpbq && !a16;  // LPBQ expanded in registers by the A8 GEMM
+  std::vector<uint8_t> tiles(static_cast<size_t>(sh.ncols_op) * sh.Kp, 0);
+  TileWriter tw{tiles, KT};
   if (!a16) {
     for (int n = 0; n < N; ++n)
-      for (int k = 0; k < K; ++k) {
-        int v = gemm_lpbq_regs ? d->weight_nk[static_cast<size_t>(n) * K + k] : wint[static_cast<size_t>(n) * K + k];
-        tw.put(n, k, v);
-      }
-    if (gemm_lpbq_regs) {
-      // per tile (nt, kt): [256 cols][4] -- the block scale of each 32-k chunk of the tile
-      lpbq_tiles.assign(static_cast<size_t>(sh.ncols_op / kBN) * KT * kBN * 4, 1);
-      for (int n = 0; n < N; ++n)
-        for (int k32 = 0; k32 < K / 32; ++k32) {
-          const size_t tile = static_cast<size_t>(n / kBN) * KT + (k32 * 32) / kBK;
-          lpbq_tiles[tile * (kBN * 4) + (n % kBN) * 4 + (k32 & 3)] =
-              d->lpbq_block_scale[static_cast<size_t>(n) * nblk + (k32 * 32) / bs];
-        }
-    }
+      for (int k = 0; k < K; ++k) tw.put(n, k, wint[static_cast<size_t>(n) * K + k]);
   } else {
     for (int n = 0; n < N; ++n) {
       const int cq = (n / 32) * 64 + (n % 32), cr = cq + 32;
@@ -329,7 +300,6 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   QmmDevice &D = p->dev;
   std::memset(&D, 0, sizeof(D));
   if (st == QH_STATUS_OK) st = al.upload(&D.tiles, tiles);
-  if (st == QH_STATUS_OK) st = al.upload(&D.lpbq_tiles, lpbq_tiles);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_tiles, gemv_tiles);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_lpbq, gemv_lpbq);
   if (st == QH_STATUS_OK) st = al.upload(&D.alpha, alpha);
@@ -352,7 +322,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     return st;
   }
   p->device_bytes = al.bytes;
-  p->gemm_weight_bytes = tiles.size() + lpbq_tiles.size();
+  p->gemm_weight_bytes = tiles.size();
   // Bytes one GEMV call must stream: packed codes (+ block scales) of the logical N x K.
   {
     const uint64_t codes = static_cast<uint64_t>(N) * K / (sh.gemv_fmt == kTileI8 ? 1 : 2);
