@@ -302,7 +302,7 @@ def main() -> int:
                    "m": M, "k": K, "n": N, "family": "w4a8_per_channel"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": I8_PEAK_TOPS, "unit": "TOPS",
                      "frac": round(tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("w4a8_gemm_4096"),
-                     "kernel": "qmm_gemm_kernel<A8, int4 tiles>", "measured": "stream events over the timed steps"},
+                     "kernel": "qmm_gemm_kernel<A8> (int8 weight tiles)", "measured": "stream events over the timed steps"},
         "extra": extra,
     }
     if not args.quick and not args.only:
