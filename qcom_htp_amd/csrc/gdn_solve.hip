@@ -9,7 +9,9 @@
 //         X_I = T_II G                         (MFMA)
 //      -- the block merge T_ij = T_ii * sum_{k=j}^{i-1} A_ik T_kj of the reference core
 //      (example/gdn_native/solve_op/src/gdn_solve_core.h:55-75), evaluated column-panel-wise.
-// The next row block of A is prefetched into registers while the current block is multiplied.
+// The next two row blocks of A are prefetched into registers while the current block is
+// multiplied, and the barriers wait for LDS traffic only, so the chain of dependent block steps
+// is not paced by global-memory latency.
 // Precision: QH_GDN_FP32 uses v_mfma_f32_16x16x4_f32; QH_GDN_BF16 feeds the G products through
 // v_mfma_f32_16x16x32_bf16 (fp32 accumulation) and keeps the diagonal solves and T_II G in fp32.
 // The u16 variant applies the GdnSolve op's code contract on load / store
@@ -24,6 +26,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int kGdnThreads = 256;
+
+// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS operations only.
+// __syncthreads() would also wait for the row-block prefetches in flight (its release fence).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 constexpr int kMaxNb = 16;  // C <= 256
 
 struct GdnArgs {
@@ -87,6 +93,32 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
     store_t<U16>(g, hbase + static_cast<size_t>(r) * C + c0 + c, 0.0f);
   }
 
+  float4 pre0[4], pre1[4];
+  auto prefetch = [&](int I, float4 (&pre)[4]) {
+    const int L = 16 * (I - J), q = L / 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = t + u * kGdnThreads;
+      if (e < 16 * q) {
+        const int r = e / q, c4 = e % q;
+        pre[u] = load_a4<U16>(g, hbase + static_cast<size_t>(I * 16 + r) * C + c0 + 4 * c4);
+      }
+    }
+  };
+  auto commit = [&](int I, const float4 (&pre)[4]) {
+    const int L = 16 * (I - J), q = L / 4;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = t + u * kGdnThreads;
+      if (e < 16 * q) {
+        const int r = e / q, c4 = e % q;
+        abuf[r][4 * c4 + 0] = pre[u].x;
+        abuf[r][4 * c4 + 1] = pre[u].y;
+        abuf[r][4 * c4 + 2] = pre[u].z;
+        abuf[r][4 * c4 + 3] = pre[u].w;
+      }
+    }
+  };
   // ---- diagonal inverses T_II, I = J .. nb-1 ----------------------------------------------
   for (int base = J; base < nb; base += 16) {
     // stage the 16x16 diagonal blocks of this round
@@ -95,7 +127,11 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
       const int I = base + b;
       if (I < nb) abuf[i][b * 16 + k] = load_a<U16>(g, hbase + static_cast<size_t>(I * 16 + i) * C + I * 16 + k);
     }
-    __syncthreads();
+    if (base == J) {  // the first two row blocks of the chain load under the diagonal solves
+      if (J + 1 < nb) prefetch(J + 1, pre0);
+      if (J + 2 < nb) prefetch(J + 2, pre1);
+    }
+    lds_barrier();
     const int b = wave * 4 + (lane >> 4), j = lane & 15;
     const int I = base + b;
     if (I < nb) {
@@ -110,7 +146,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) tdiag[I - J][i][j] = x[i];
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   // ---- X_J = T_JJ ----------------------------------------------------------------------------
@@ -123,39 +159,15 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
 
   // ---- block forward substitution down the panel -------------------------------------------
   // Row block I needs A[16I .. 16I+15][c0 .. 16I-1]: 16 rows x L columns, L = 16 (I - J).
-  // Each thread prefetches up to 4 float4 of the next block (16 * 240 / 4 / 256 < 4).
-  float4 pre[4];
-  auto prefetch = [&](int I) {
-    const int L = 16 * (I - J), q = L / 4;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = t + u * kGdnThreads;
-      if (e < 16 * q) {
-        const int r = e / q, c4 = e % q;
-        pre[u] = load_a4<U16>(g, hbase + static_cast<size_t>(I * 16 + r) * C + c0 + 4 * c4);
-      }
-    }
-  };
-  auto commit = [&](int I) {
-    const int L = 16 * (I - J), q = L / 4;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = t + u * kGdnThreads;
-      if (e < 16 * q) {
-        const int r = e / q, c4 = e % q;
-        abuf[r][4 * c4 + 0] = pre[u].x;
-        abuf[r][4 * c4 + 1] = pre[u].y;
-        abuf[r][4 * c4 + 2] = pre[u].z;
-        abuf[r][4 * c4 + 3] = pre[u].w;
-      }
-    }
-  };
-  if (J + 1 < nb) prefetch(J + 1);
-  for (int I = J + 1; I < nb; ++I) {
-    __syncthreads();  // xs rows of the previous block visible; abuf free
-    commit(I);
-    __syncthreads();
-    if (I + 1 < nb) prefetch(I + 1);
+  // Each thread holds up to 4 float4 of a block (16 * 240 / 4 / 256 < 4); two blocks are in
+  // flight ahead of the one being multiplied.
+  // Row blocks alternate between the two prefetch slots (a register copy between slots would
+  // wait for the load in flight).
+  auto step = [&](const int I, float4 (&pre)[4]) __attribute__((always_inline)) {
+    lds_barrier();  // xs rows of the previous block visible; abuf free
+    commit(I, pre);
+    lds_barrier();
+    if (I + 2 < nb) prefetch(I + 2, pre);  // the slot just committed takes block I + 2
     const int L = 16 * (I - J);
     // partial G over this wave's 16-wide K blocks
     v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -185,7 +197,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) gpart[wave][4 * kq + q][r] = acc[q];
-    __syncthreads();
+    lds_barrier();
     if (wave == 0) {
       // G (summed over waves) as the B operand of X_I = T_II G
       v4f x = {0.f, 0.f, 0.f, 0.f};
@@ -202,6 +214,10 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
         store_t<U16>(g, hbase + static_cast<size_t>(I * 16 + row) * C + c0 + r, x[q]);
       }
     }
+  };
+  for (int I = J + 1; I < nb; I += 2) {
+    step(I, pre0);
+    if (I + 1 < nb) step(I + 1, pre1);
   }
 }
 
