@@ -8,17 +8,17 @@
 // Decomposition.  T is never formed.  U and W solve (I - A) X = R with the 256 right-hand-side
 // columns R = [beta V | beta K^ (e^g)], by block forward substitution over 16-row blocks:
 //     X_I = T_II (R_I + sum_{J<I} A_IJ X_J),   T_II = (I - A_II)^-1 (16 x 16).
-// Two workgroups per (batch, chunk, head): one solves the U columns, one the W columns; each
-// builds A itself (the A-build is a sixth of the work, and the split halves the LDS and
-// register footprint).  Inside a workgroup:
-//   1. K^ (bf16) into LDS, row-swizzled; g cumsum and beta into LDS;
+// One workgroup per (batch, chunk, head), persistent over items:
+//   1. K^ (bf16) into LDS, row-swizzled, with 1 / |k| per row; g cumsum and beta into LDS;
 //   2. the lower 16 x 16 blocks of K^ K^T with v_mfma_f32_16x16x32_bf16 (blocks spread over the
-//      4 waves), scaled to A: strictly-lower blocks stored bf16, diagonal blocks fp32;
+//      waves), scaled to A: strictly-lower blocks stored bf16, diagonal blocks fp32;
 //   3. T_II for all diagonal blocks by forward substitution (one lane per column), in place;
-//   4. the U workgroup replaces K^ in LDS by V; then each wave solves 32 of the 128 columns:
-//      A_IJ X_J with v_mfma_f32_16x16x16_bf16 (X_J kept in registers in the layout that MFMA
-//      reads as its B operand, which is the layout the MFMA result comes out in), T_II times
-//      the sum with v_mfma_f32_16x16x4_f32, results stored to HBM as they are produced.
+//   4. all 256 right-hand-side columns (W's 128, then U's 128) as 16-column tiles over the
+//      waves: A_IJ X_J with v_mfma_f32_16x16x16_bf16 (X_J kept in registers in the layout that
+//      MFMA reads as its B operand, which is the layout the MFMA result comes out in), T_II
+//      times the sum with v_mfma_f32_16x16x4_f32, results stored to HBM as they are produced.
+//      The right-hand-side rows come from global memory (the keys were just read, so from L2),
+//      one block step ahead, scaled on the fly: beta / |k| [e^g] for W, beta for U.
 // Precision: bf16 operands, fp32 accumulation; diagonal inverses and T_II products in fp32.
 
 #include "qmm_internal.h"
@@ -53,46 +53,54 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 // the same chunk hit distinct banks).
 __device__ __forceinline__ int kofs(int row, int d) { return row * 256 + 16 * ((d >> 3) ^ (row & 15)) + 2 * (d & 7); }
 
+// c ? x : y for two kernel-argument pointers, kept in SGPRs, as a global-memory pointer.  Both
+// are materialised first so that the choice does not become a dynamically indexed load of the
+// argument block.
+template <typename T>
+using gptr = __attribute__((address_space(1))) T *;
+template <typename T>
+__device__ __forceinline__ gptr<T> pick_ptr(bool c, const void *x, const void *y) {
+  uint64_t xi = reinterpret_cast<uint64_t>(x), yi = reinterpret_cast<uint64_t>(y);
+  asm volatile("" : "+s"(xi));
+  asm volatile("" : "+s"(yi));
+  return (gptr<T>)(reinterpret_cast<T *>(c ? xi : yi));
+}
+
 __device__ __forceinline__ size_t tok_index(const ChunkArgs &a, int b, int tok, int h) {
   return (static_cast<size_t>(b) * a.T + tok) * a.H + h;
 }
 
-// The role of a workgroup is fixed: items blockIdx.x + k * gridDim.x with gridDim.x a multiple
-// of 16 all have bit 3 of the item index equal to bit 3 of blockIdx.x.
 // Workgroup size: 8 waves (two per SIMD) for C >= 128, 4 waves for C = 64.
 template <int NB>
 constexpr int chunk_threads() { return NB >= 8 ? 512 : 256; }
 
-template <int NB, int ROLE>
+template <int NB>
 __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems, uint8_t *smat, uint16_t *ablk,
-                                            float *adiag, float *gs, float *bs, float *wsum) {
+                                            float *adiag, float *gs, float *bs, float *rn, float *wsc, float *wsum) {
   constexpr int C = NB * 16;
   constexpr int kChunkThreads = chunk_threads<NB>();
   constexpr int kWaves = kChunkThreads / 64;
-  constexpr int kTiles = 8 / kWaves;  // 16-column tiles of the 128 right-hand sides per wave
+  constexpr int kTiles = 16 / kWaves;  // 16-column tiles of the 256 right-hand sides per wave
+  constexpr int kChains = kTiles >= 4 ? 1 : 4 / kTiles;
   constexpr int kRowPasses = C / (kChunkThreads / 8);   // K rows: 8 lanes per row
-  constexpr int kVPasses = C / (kChunkThreads / 16);    // V rows: 16 lanes per row
-  static_assert(kRowPasses >= 1 && kVPasses >= 1, "chunk too small for the workgroup");
+  static_assert(kRowPasses >= 1, "chunk too small for the workgroup");
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int q = lane >> 4, l16 = lane & 15;
 
-  // Work item -> (batch, chunk, head).  The two roles of one (batch, chunk, head) differ by 8
-  // in the item index, so workgroups w and w + 8 of the persistent grid (one XCD) run them
-  // together and share the key rows in L2.
+  // Work item -> (batch, chunk, head).
   struct Item {
     int b, c, h;
     bool valid;
   };
   auto item_of = [&](int it) __attribute__((always_inline)) {
     Item r;
-    const int ch_idx = ((it >> 4) << 3) | (it & 7);
-    r.h = ch_idx % a.H;
-    const int rest = ch_idx / a.H;
+    r.h = it % a.H;
+    const int rest = it / a.H;
     r.c = rest % a.nchunks;
     r.b = rest / a.nchunks;
-    r.valid = it < nitems && r.b < a.B;
+    r.valid = it < nitems;
     return r;
   };
   // Key rows, g and beta of an item into registers (all loads in flight together).
@@ -146,6 +154,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       ss += __shfl_xor(ss, 2, 64);
       ss += __shfl_xor(ss, 4, 64);
       const float inv = 1.0f / sqrtf(ss + 1e-6f);
+      if (part == 0) rn[row] = inv;
       uint32_t o[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = f32_to_bf16(f[2 * i] * inv) | (f32_to_bf16(f[2 * i + 1] * inv) << 16);
@@ -156,7 +165,10 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     if (t < C) {
       float pre = 0.0f;
       for (int w = 0; w < (t >> 6); ++w) pre += wsum[w];
-      gs[t] = gv + pre;
+      const float gt = gv + pre;
+      gs[t] = gt;
+      // scale of row t of W's right-hand side: beta / |k| [e^g]
+      wsc[t] = bpre * rn[t] * (a.decay_w ? __expf(gt) : 1.0f);
     }
     __syncthreads();
 
@@ -208,16 +220,26 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     }
     __syncthreads();
 
-    // The U role reads its values into registers now; the next item's keys are prefetched;
-    // both sets of loads run under the diagonal inverses.
-    uint4 vr[ROLE == 0 ? kVPasses : 1];
-    if (ROLE == 0) {
+    // The first block row of right-hand sides and the next item's keys load under the diagonal
+    // inverses.  Tile tg of the 256 right-hand-side columns: tg < 8 are W's (keys), the rest
+    // U's (values); lane column d = (tg % 8) * 16 + l16, rows 4q .. 4q + 3 of the block row.
+    // The columns of a wave all belong to W or all to U.  Element offsets fit in 32 bits
+    // (B * T * H * 128 <= 2^31 is checked at the boundary).
+    const bool is_w = wave * kTiles < 8;
+    const gptr<const uint16_t> rsrc = pick_ptr<const uint16_t>(is_w, a.k, a.v);
+    const uint32_t tstride = static_cast<uint32_t>(a.H) * kD;  // elements per token
+    const uint32_t lbase =
+        (static_cast<uint32_t>(b * a.T + tok0 + 4 * q) * static_cast<uint32_t>(a.H) + h) * kD + l16;
+    uint32_t rraw[2][kTiles][4];
+    auto rhs_load = [&](int I, uint32_t (&r)[kTiles][4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int p = 0; p < kVPasses; ++p) {
-        const int row = p * (kChunkThreads / 16) + (t >> 4), part = t & 15;
-        vr[p] = *reinterpret_cast<const uint4 *>(a.v + tok_index(a, b, tok0 + row, h) * kD + part * 8);
+      for (int tl = 0; tl < kTiles; ++tl) {
+        const uint32_t dcol = ((wave * kTiles + tl) & 7) * 16;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) r[tl][s] = rsrc[lbase + dcol + (I * 16 + s) * tstride];
       }
-    }
+    };
+    rhs_load(0, rraw[0]);
     it += gridDim.x;
     const Item nxt = item_of(it);
     prefetch(nxt);
@@ -237,35 +259,25 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
 #pragma unroll
       for (int r = 0; r < 16; ++r) adiag[I * 256 + r * 16 + col] = x[r];
     }
-    if (ROLE == 0) {
-#pragma unroll
-      for (int p = 0; p < kVPasses; ++p) {
-        const int row = p * (kChunkThreads / 16) + (t >> 4), part = t & 15;
-        *reinterpret_cast<uint4 *>(smat + kofs(row, part * 8)) = vr[p];
-      }
-    }
     __syncthreads();
 
     // ---- 4. X_I = T_II (R_I + sum_{J<I} A_IJ X_J), 16 * kTiles columns per wave ------------
-    const bool decay = ROLE == 1 && a.decay_w;
+    const float *const rsc = is_w ? wsc : bs;
+    const gptr<float> of = pick_ptr<float>(is_w, a.w, a.u);
+    const gptr<uint16_t> oh = pick_ptr<uint16_t>(is_w, a.w, a.u);
     v4s xb[NB][kTiles];  // X_J in bf16, the MFMA B-operand layout (= result layout)
-    float *const wf = static_cast<float *>(ROLE ? a.w : a.u);
-    uint16_t *const wh = static_cast<uint16_t *>(ROLE ? a.w : a.u);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      v4f acc[kTiles][4];  // four independent accumulation chains per tile (J mod 4)
+      if (I + 1 < NB) rhs_load(I + 1, rraw[(I + 1) & 1]);
+      v4f acc[kTiles][kChains];  // kTiles * kChains = 4 independent accumulation chains
 #pragma unroll
-      for (int tl = 0; tl < kTiles; ++tl) {
-        const int d = (wave * kTiles + tl) * 16 + l16;
+      for (int s = 0; s < 4; ++s) {
+        const float sc = rsc[I * 16 + 4 * q + s];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int i = I * 16 + 4 * q + s;
-          float r = bs[i] * bf16_to_f32(*reinterpret_cast<const uint16_t *>(smat + kofs(i, d)));
-          if (decay) r *= __expf(gs[i]);
-          acc[tl][0][s] = r;
-          acc[tl][1][s] = 0.0f;
-          acc[tl][2][s] = 0.0f;
-          acc[tl][3][s] = 0.0f;
+        for (int tl = 0; tl < kTiles; ++tl) {
+          acc[tl][0][s] = sc * bf16_to_f32(rraw[I & 1][tl][s]);
+#pragma unroll
+          for (int c = 1; c < kChains; ++c) acc[tl][c][s] = 0.0f;
         }
       }
 #pragma unroll
@@ -273,27 +285,30 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
         const uint2 ap = *reinterpret_cast<const uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q);
 #pragma unroll
         for (int tl = 0; tl < kTiles; ++tl)
-          acc[tl][J & 3] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, ap), xb[J][tl], acc[tl][J & 3], 0, 0, 0);
+          acc[tl][J % kChains] =
+              __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, ap), xb[J][tl], acc[tl][J % kChains], 0, 0, 0);
       }
       const float4 tr = *reinterpret_cast<const float4 *>(adiag + I * 256 + l16 * 16 + 4 * q);
       const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
 #pragma unroll
       for (int tl = 0; tl < kTiles; ++tl) {
-        const v4f sum = (acc[tl][0] + acc[tl][1]) + (acc[tl][2] + acc[tl][3]);
+        v4f sum = acc[tl][0];
+#pragma unroll
+        for (int c = 1; c < kChains; ++c) sum += acc[tl][c];
         v4f x = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) x = __builtin_amdgcn_mfma_f32_16x16x4f32(trv[s], sum[s], x, 0, 0, 0);
         const uint32_t p0 = f32_to_bf16(x[0]) | (f32_to_bf16(x[1]) << 16);
         const uint32_t p1 = f32_to_bf16(x[2]) | (f32_to_bf16(x[3]) << 16);
         xb[I][tl] = __builtin_bit_cast(v4s, make_uint2(p0, p1));
-        const int d = (wave * kTiles + tl) * 16 + l16;
+        const uint32_t dcol = ((wave * kTiles + tl) & 7) * 16;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const size_t o = tok_index(a, b, tok0 + I * 16 + 4 * q + s, h) * kD + d;
+          const uint32_t o = lbase + dcol + (I * 16 + s) * tstride;
           if (a.out_f32)
-            wf[o] = x[s];
+            of[o] = x[s];
           else
-            wh[o] = static_cast<uint16_t>(s < 2 ? (s == 0 ? p0 & 0xFFFFu : p0 >> 16) : (s == 2 ? p1 & 0xFFFFu : p1 >> 16));
+            oh[o] = static_cast<uint16_t>(s < 2 ? (s == 0 ? p0 & 0xFFFFu : p0 >> 16) : (s == 2 ? p1 & 0xFFFFu : p1 >> 16));
         }
       }
     }
@@ -306,22 +321,19 @@ template <int NB>
 __global__ __launch_bounds__(chunk_threads<NB>(), 1) void gdn_chunk_kernel(const ChunkArgs a, const int nitems) {
   constexpr int C = NB * 16;
   constexpr int kLowBlocks = NB * (NB - 1) / 2;
-  __shared__ __attribute__((aligned(16))) uint8_t smat[C * 256];             // K^, then V (U role)
+  __shared__ __attribute__((aligned(16))) uint8_t smat[C * 256];             // K^
   __shared__ __attribute__((aligned(16))) uint16_t ablk[(kLowBlocks > 0 ? kLowBlocks : 1) * 256];  // A_IJ, I > J
   __shared__ __attribute__((aligned(16))) float adiag[NB * 256];             // A_II, then T_II
-  __shared__ float gs[C], bs[C], wsum[8];
-  if ((blockIdx.x >> 3) & 1)
-    chunk_items<NB, 1>(a, nitems, smat, ablk, adiag, gs, bs, wsum);
-  else
-    chunk_items<NB, 0>(a, nitems, smat, ablk, adiag, gs, bs, wsum);
+  __shared__ float gs[C], bs[C], rn[C], wsc[C], wsum[8];
+  chunk_items<NB>(a, nitems, smat, ablk, adiag, gs, bs, rn, wsc, wsum);
 }
 
 template <int NB>
 qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
-  const long long pairs = static_cast<long long>(a.B) * a.nchunks * a.H;
-  const long long items = (pairs + 7) / 8 * 16;  // groups of 8 (batch, chunk, head) x 2 roles
+  const long long items = static_cast<long long>(a.B) * a.nchunks * a.H;  // (batch, chunk, head)
   if (items > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: too many chunks");
-  // Persistent grid: as many workgroups as fit on the device at once, a multiple of 16.
+  if (items == 0) return QH_STATUS_OK;
+  // Persistent grid: as many workgroups as fit on the device at once.
   static int slots[17] = {0};
   int dev = 0;
   (void)hipGetDevice(&dev);
@@ -333,8 +345,7 @@ qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
     if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute");
     slots[NB] = (per_cu < 1 ? 1 : per_cu) * cus;
   }
-  long long grid = slots[NB] / 16 * 16;
-  if (grid < 16) grid = 16;
+  long long grid = slots[NB];
   if (grid > items) grid = items;
   hipLaunchKernelGGL(gdn_chunk_kernel<NB>, dim3(static_cast<unsigned>(grid)), dim3(chunk_threads<NB>()), 0, stream, a,
                      static_cast<int>(items));
