@@ -21,12 +21,16 @@
 //      one block step ahead, scaled on the fly: beta / |k| [e^g] for W, beta for U.
 // Precision: bf16 operands, fp32 accumulation; diagonal inverses and T_II products in fp32.
 
+#include <atomic>
+
 #include "qmm_internal.h"
 
 namespace qh {
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
@@ -40,13 +44,29 @@ struct ChunkArgs {
   int decay_w, out_f32;
 };
 
+// Workgroup barrier for LDS traffic only (does not wait for outstanding global memory operations).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-// float -> bf16 bits, round to nearest even (inputs are finite)
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 (a in the low half), round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2bf));
 }
+
+// Four floats as bf16 hi (round to nearest even) and lo = bf16(f - hi): the 8-element MFMA
+// operand {hi0..hi3, lo0..lo3}; hi + lo carries about 16 significant bits.
+__device__ __forceinline__ v8bf split_bf16x4(const float4 f) {
+  const uint32_t h01 = pack_bf16(f.x, f.y), h23 = pack_bf16(f.z, f.w);
+  const uint32_t l01 = pack_bf16(f.x - __uint_as_float(h01 << 16), f.y - __uint_as_float(h01 & 0xFFFF0000u));
+  const uint32_t l23 = pack_bf16(f.z - __uint_as_float(h23 << 16), f.w - __uint_as_float(h23 & 0xFFFF0000u));
+  return __builtin_bit_cast(v8bf, make_uint4(h01, h23, l01, l23));
+}
+
+// First pair of blocks of block row I in the pair layout: sum over I' < I of ceil(I' / 2).
+__host__ __device__ constexpr int pair_base(int I) { return (I / 2) * (I / 2) + (I & 1) * (I / 2); }
 
 // Byte offset of element (row, d) of a [C][128] bf16 matrix in LDS: each 256-byte row holds 16
 // chunks of 8 elements, chunk c stored at position c ^ (row & 15) (16 consecutive rows reading
@@ -74,7 +94,7 @@ __device__ __forceinline__ size_t tok_index(const ChunkArgs &a, int b, int tok, 
 template <int NB>
 constexpr int chunk_threads() { return NB >= 8 ? 512 : 256; }
 
-template <int NB>
+template <int NB, bool OUT_F32>
 __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems, uint8_t *smat, uint16_t *ablk,
                                             float *adiag, float *gs, float *bs, float *rn, float *wsc, float *wsum) {
   constexpr int C = NB * 16;
@@ -82,8 +102,17 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
   constexpr int kWaves = kChunkThreads / 64;
   constexpr int kTiles = 16 / kWaves;  // 16-column tiles of the 256 right-hand sides per wave
   constexpr int kChains = kTiles >= 4 ? 1 : 4 / kTiles;
+  static_assert(pair_base(NB) * 1024 <= C * 256, "A' pairs must fit in smat");
   constexpr int kRowPasses = C / (kChunkThreads / 8);   // K rows: 8 lanes per row
+  // Right-hand-side prefetch distance in block rows: deep enough that a row's loads (from HBM
+  // for the values) land before the substitution reaches it; all rows for C <= 128.
+  constexpr int kDepth = NB < 8 ? NB : 8;
+  // Substitution row at whose start the next item's keys are prefetched (0: before the
+  // diagonal inverses), once enough right-hand-side registers have been freed.
+  constexpr int kKeyRow = NB > kDepth ? kDepth : 0;
+  constexpr int kWords = kTiles / 2;                    // 32-bit words of a lane's right-hand-side row
   static_assert(kRowPasses >= 1, "chunk too small for the workgroup");
+  static_assert(kTiles == 2 || kTiles == 4, "tile pairing");
 
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -94,20 +123,23 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     int b, c, h;
     bool valid;
   };
+  // An index past the end yields the last item, marked invalid (its loads stay in bounds).
   auto item_of = [&](int it) __attribute__((always_inline)) {
     Item r;
-    r.h = it % a.H;
-    const int rest = it / a.H;
+    const int ic = it < nitems ? it : nitems - 1;
+    r.h = ic % a.H;
+    const int rest = ic / a.H;
     r.c = rest % a.nchunks;
     r.b = rest / a.nchunks;
     r.valid = it < nitems;
     return r;
   };
-  // Key rows, g and beta of an item into registers (all loads in flight together).
+  // Key rows, g and beta of an item into registers (all loads in flight together).  Issued for
+  // an invalid item too (the last item again): branch-free, so the compiler counts the
+  // outstanding loads exactly.
   uint4 kr[kRowPasses][2];
   float gpre = 0.0f, bpre = 0.0f;
   auto prefetch = [&](const Item &it) __attribute__((always_inline)) {
-    if (!it.valid) return;
 #pragma unroll
     for (int p = 0; p < kRowPasses; ++p) {
       const int row = p * (kChunkThreads / 8) + (t >> 3), part = t & 7;
@@ -115,19 +147,15 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       kr[p][0] = src[0];
       kr[p][1] = src[1];
     }
-    if (t < C) {
-      const size_t ix = tok_index(a, it.b, it.c * C + t, it.h);
+    {  // every lane loads (rows clamped), so that the count of outstanding loads is uniform
+      const size_t ix = tok_index(a, it.b, it.c * C + (t < C ? t : C - 1), it.h);
       gpre = a.g[ix];
       bpre = a.beta[ix];
     }
   };
 
-  int it = blockIdx.x;
-  Item cur = item_of(it);
-  prefetch(cur);
-  while (cur.valid) {
-    const int b = cur.b, h = cur.h, tok0 = cur.c * C;
-    // ---- 1. g cumsum, beta, K^ -------------------------------------------------------------
+  // ---- 1. g cumsum, beta, K^ (from the prefetched registers) ---------------------------------
+  auto phase1 = [&]() __attribute__((always_inline)) {
     float gv = t < C ? gpre : 0.0f;
     if (t < C) bs[t] = bpre;
 #pragma unroll
@@ -157,11 +185,11 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       if (part == 0) rn[row] = inv;
       uint32_t o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = f32_to_bf16(f[2 * i] * inv) | (f32_to_bf16(f[2 * i + 1] * inv) << 16);
+      for (int i = 0; i < 8; ++i) o[i] = pack_bf16(f[2 * i] * inv, f[2 * i + 1] * inv);
       *reinterpret_cast<uint4 *>(smat + kofs(row, part * 16)) = make_uint4(o[0], o[1], o[2], o[3]);
       *reinterpret_cast<uint4 *>(smat + kofs(row, part * 16 + 8)) = make_uint4(o[4], o[5], o[6], o[7]);
     }
-    __syncthreads();
+    lds_barrier();
     if (t < C) {
       float pre = 0.0f;
       for (int w = 0; w < (t >> 6); ++w) pre += wsum[w];
@@ -170,25 +198,36 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       // scale of row t of W's right-hand side: beta / |k| [e^g]
       wsc[t] = bpre * rn[t] * (a.decay_w ? __expf(gt) : 1.0f);
     }
-    __syncthreads();
+    lds_barrier();
+  };
 
+  // Phase 1 of the next item runs at the end of the current one, in straight-line code after the
+  // substitution's loads and stores, so that waiting for the prefetched keys does not wait for
+  // those (the outstanding-load count is in issue order).
+  int it = blockIdx.x;
+  Item cur = item_of(it);
+  prefetch(cur);
+  phase1();
+  while (cur.valid) {
+    const int b = cur.b, h = cur.h, tok0 = cur.c * C;
     // ---- 2. A = -beta_i (K^ K^T)_ij e^{g_i - g_j}, lower blocks -----------------------------
-    // Wave w takes the block rows w and NB-1-w (NB+1 blocks, balanced).  For block (I, J) the
-    // MFMA computes D = K^_J K^_I^T = G_IJ^T, so each lane holds row l16 of G_IJ, columns
-    // 4q .. 4q+3; the fragments of K^_I are read once per row, two J chains run together.
-    auto a_store = [&](int I, int J, const v4f &acc) __attribute__((always_inline)) {
-      const int i = I * 16 + l16;
-      const float bi = bs[i], gi = gs[i];
+    // Wave w < NB/2 takes the block rows I0 = w and I1 = NB-1-w (NB+1 blocks, balanced): the
+    // key fragments of block row J (the MFMA B operand) are read once for both rows and
+    // prefetched one J ahead.  For block (I, J) the MFMA computes D = K^_I K^_J^T = G_IJ, so each
+    // lane holds rows 4q .. 4q+3 of column l16; blocks are stored column-major (element (r, c)
+    // at c * 16 + r).
+    auto a_store = [&](int I, int J, float gj, const float4 &b4, const float4 &g4, const v4f &acc)
+                       __attribute__((always_inline)) {
+      const float bi[4] = {b4.x, b4.y, b4.z, b4.w}, gi[4] = {g4.x, g4.y, g4.z, g4.w};
       float av[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int j = J * 16 + 4 * q + s;
-        av[s] = i > j ? -bi * acc[s] * __expf(gi - gs[j]) : 0.0f;
+        const bool low = I > J || 4 * q + s > l16;  // i > j
+        av[s] = low ? -bi[s] * acc[s] * __expf(gi[s] - gj) : 0.0f;
       }
       if (I > J) {
-        const uint32_t p0 = f32_to_bf16(av[0]) | (f32_to_bf16(av[1]) << 16);
-        const uint32_t p1 = f32_to_bf16(av[2]) | (f32_to_bf16(av[3]) << 16);
-        *reinterpret_cast<uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q) = make_uint2(p0, p1);
+        *reinterpret_cast<uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q) =
+            make_uint2(pack_bf16(av[0], av[1]), pack_bf16(av[2], av[3]));
       } else {
         *reinterpret_cast<float4 *>(adiag + I * 256 + l16 * 16 + 4 * q) = make_float4(av[0], av[1], av[2], av[3]);
       }
@@ -197,52 +236,74 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       const int r = row_blk * 16 + l16, ch = kk * 4 + q;
       return __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(smat + r * 256 + 16 * (ch ^ (r & 15))));
     };
-    if (wave < (NB + 1) / 2) {
+    if (wave < NB / 2) {
+      const int I0 = wave, I1 = NB - 1 - wave;
+      v8bf f0[kD / 32], f1[kD / 32], fa[kD / 32], fb[kD / 32];
 #pragma unroll
-      for (int side = 0; side < 2; ++side) {
-        const int I = side == 0 ? wave : NB - 1 - wave;
-        if (side == 1 && I == wave) break;  // NB odd: the middle row once
-        v8bf bi[kD / 32];
+      for (int kk = 0; kk < kD / 32; ++kk) {
+        f0[kk] = frag(I0, kk);
+        f1[kk] = frag(I1, kk);
+        fa[kk] = frag(0, kk);
+      }
+      const float4 b0 = *reinterpret_cast<const float4 *>(bs + I0 * 16 + 4 * q);
+      const float4 g0 = *reinterpret_cast<const float4 *>(gs + I0 * 16 + 4 * q);
+      const float4 b1 = *reinterpret_cast<const float4 *>(bs + I1 * 16 + 4 * q);
+      const float4 g1 = *reinterpret_cast<const float4 *>(gs + I1 * 16 + 4 * q);
+      float gja = gs[l16], gjb = 0.0f;
+      auto step = [&](int J, const v8bf (&cur)[kD / 32], float gjc, v8bf (&nxt)[kD / 32], float &gjn)
+                      __attribute__((always_inline)) {
+        const int Jn = J + 1 <= I1 ? J + 1 : I1;  // clamped: the loads stay branch-free
 #pragma unroll
-        for (int kk = 0; kk < kD / 32; ++kk) bi[kk] = frag(I, kk);
-        for (int J = 0; J <= I; J += 2) {
-          const bool two = J + 1 <= I;
-          v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kk = 0; kk < kD / 32; ++kk) nxt[kk] = frag(Jn, kk);
+        gjn = gs[Jn * 16 + l16];
+        v4f acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-          for (int kk = 0; kk < kD / 32; ++kk) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(J, kk), bi[kk], acc0, 0, 0, 0);
-            if (two) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag(J + 1, kk), bi[kk], acc1, 0, 0, 0);
-          }
-          a_store(I, J, acc0);
-          if (two) a_store(I, J + 1, acc1);
+        for (int kk = 0; kk < kD / 32; ++kk) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f1[kk], cur[kk], acc1, 0, 0, 0);
+        if (J <= I0) {
+          v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int kk = 0; kk < kD / 32; ++kk) acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f0[kk], cur[kk], acc0, 0, 0, 0);
+          a_store(I0, J, gjc, b0, g0, acc0);
         }
+        a_store(I1, J, gjc, b1, g1, acc1);
+      };
+      for (int J = 0; J <= I1; J += 2) {
+        step(J, fa, gja, fb, gjb);
+        if (J + 1 <= I1) step(J + 1, fb, gjb, fa, gja);
       }
     }
-    __syncthreads();
+    lds_barrier();
 
-    // The first block row of right-hand sides and the next item's keys load under the diagonal
-    // inverses.  Tile tg of the 256 right-hand-side columns: tg < 8 are W's (keys), the rest
-    // U's (values); lane column d = (tg % 8) * 16 + l16, rows 4q .. 4q + 3 of the block row.
-    // The columns of a wave all belong to W or all to U.  Element offsets fit in 32 bits
+    // Right-hand sides.  A wave owns kTiles 16-column tiles, all of W (keys) or all of U
+    // (values): the 16 * kTiles adjacent columns from cb = ((wave * kTiles) % 8) * 16, column
+    // cb + kTiles * l16 + tl in tile tl, so that a lane reads (and writes) its kTiles columns of
+    // a row in one access; lane rows 4q .. 4q + 3 of a block row.  The first kDepth block rows
+    // load under the diagonal inverses.  Element offsets fit in 32 bits
     // (B * T * H * 128 <= 2^31 is checked at the boundary).
     const bool is_w = wave * kTiles < 8;
     const gptr<const uint16_t> rsrc = pick_ptr<const uint16_t>(is_w, a.k, a.v);
     const uint32_t tstride = static_cast<uint32_t>(a.H) * kD;  // elements per token
-    const uint32_t lbase =
-        (static_cast<uint32_t>(b * a.T + tok0 + 4 * q) * static_cast<uint32_t>(a.H) + h) * kD + l16;
-    uint32_t rraw[2][kTiles][4];
-    auto rhs_load = [&](int I, uint32_t (&r)[kTiles][4]) __attribute__((always_inline)) {
+    const uint32_t lbase = (static_cast<uint32_t>(b * a.T + tok0 + 4 * q) * static_cast<uint32_t>(a.H) + h) * kD +
+                           ((wave * kTiles) & 7) * 16 + kTiles * l16;
+    uint32_t rraw[kDepth + 1][4][kWords];
+    auto rhs_load = [&](int I, uint32_t (&r)[4][kWords]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int tl = 0; tl < kTiles; ++tl) {
-        const uint32_t dcol = ((wave * kTiles + tl) & 7) * 16;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) r[tl][s] = rsrc[lbase + dcol + (I * 16 + s) * tstride];
+      for (int s = 0; s < 4; ++s) {
+        const gptr<const uint16_t> src = rsrc + lbase + (I * 16 + s) * tstride;
+        if constexpr (kWords == 1) {
+          r[s][0] = *(gptr<const uint32_t>)src;
+        } else {
+          const v2u v = *(gptr<const v2u>)src;
+          r[s][0] = v[0];
+          r[s][1] = v[1];
+        }
       }
     };
-    rhs_load(0, rraw[0]);
+#pragma unroll
+    for (int I = 0; I < kDepth && I < NB; ++I) rhs_load(I, rraw[I]);
     it += gridDim.x;
     const Item nxt = item_of(it);
-    prefetch(nxt);
+    if (kKeyRow == 0) prefetch(nxt);
 
     // ---- 3. T_II = (I - A_II)^-1, one lane per column, in place ----------------------------
     if (t < NB * 16) {
@@ -253,105 +314,168 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       for (int r = 0; r < 16; ++r) {
         float sacc = r == col ? 1.0f : 0.0f;
 #pragma unroll
-        for (int kx = 0; kx < r; ++kx) sacc = fmaf(Ad[r * 16 + kx], x[kx], sacc);
+        for (int kx = 0; kx < r; ++kx) sacc = fmaf(Ad[kx * 16 + r], x[kx], sacc);
         x[r] = sacc;
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) adiag[I * 256 + r * 16 + col] = x[r];
+      for (int r = 0; r < 16; ++r) adiag[I * 256 + r * 16 + col] = x[r];  // T_II row-major
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- 4. X_I = T_II (R_I + sum_{J<I} A_IJ X_J), 16 * kTiles columns per wave ------------
-    const float *const rsc = is_w ? wsc : bs;
+    // ---- 3b. A'_IJ = T_II A_IJ (I > J) in bf16, into smat (free after the A-build) ----------
+    // Computed transposed, D = A_IJ^T T_II^T, so that lane (q, l16) holds row l16 of A'_IJ,
+    // columns 4q .. 4q+3: the A-operand fragment of the substitution.  T_II is split into
+    // bf16 hi + lo along K (16 x 16 x 32 MFMA, K = the 16 inner indices twice).  Pair layout: the
+    // blocks (I, 2p) and (I, 2p + 1) form pair pair_base(I) + p, 1 KiB, lane-major, 16 bytes per
+    // lane (8 bytes per block); the second half of a row's last pair is zero when I is odd.
+    // Wave w < NB/2 folds the block rows w and NB-1-w: NB-1 blocks, block n of the wave is
+    // (w, n) for n < w, else (NB-1-w, n-w); all A loads are issued first.
+    if (wave < NB / 2) {
+      const int I0 = wave, I1 = NB - 1 - wave;
+      const v8bf t0 = split_bf16x4(*reinterpret_cast<const float4 *>(adiag + I0 * 256 + l16 * 16 + 4 * q));
+      const v8bf t1 = split_bf16x4(*reinterpret_cast<const float4 *>(adiag + I1 * 256 + l16 * 16 + 4 * q));
+      uint2 ac[NB - 1];
+#pragma unroll
+      for (int n = 0; n < NB - 1; ++n) {
+        const int I = n < I0 ? I0 : I1, J = n < I0 ? n : n - I0;
+        ac[n] = *reinterpret_cast<const uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q);
+      }
+#pragma unroll
+      for (int n = 0; n < NB - 1; ++n) {
+        const int I = n < I0 ? I0 : I1, J = n < I0 ? n : n - I0;
+        const v4f d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(v8bf, make_uint4(ac[n].x, ac[n].y, ac[n].x, ac[n].y)), n < I0 ? t0 : t1,
+            v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        uint8_t *const dst = smat + (pair_base(I) + (J >> 1)) * 1024 + lane * 16 + (J & 1) * 8;
+        *reinterpret_cast<uint2 *>(dst) =
+            make_uint2(pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3]));
+        if ((I & 1) && J == I - 1) *reinterpret_cast<uint2 *>(dst + 8) = make_uint2(0u, 0u);
+      }
+    }
+    lds_barrier();
+
+    // ---- 4. X_I = T'_I R_I + sum_{J<I} A'_IJ X_J,  T'_I = T_II diag(row scales) ------------
+    // One 16 x 16 x 32 MFMA per tile for T'_I R_I (T' split hi + lo, R_I raw bf16 twice) and one
+    // per pair of blocks J for the sum; only the last pair depends on X_{I-1}.
+    const float *const rsc = bs + (is_w ? C : 0);  // wsc = bs + C: one LDS object
     const gptr<float> of = pick_ptr<float>(is_w, a.w, a.u);
     const gptr<uint16_t> oh = pick_ptr<uint16_t>(is_w, a.w, a.u);
     v4s xb[NB][kTiles];  // X_J in bf16, the MFMA B-operand layout (= result layout)
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      if (I + 1 < NB) rhs_load(I + 1, rraw[(I + 1) & 1]);
-      v4f acc[kTiles][kChains];  // kTiles * kChains = 4 independent accumulation chains
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float sc = rsc[I * 16 + 4 * q + s];
+      if (I + kDepth < NB) rhs_load(I + kDepth, rraw[(I + kDepth) % (kDepth + 1)]);
+      if (kKeyRow > 0 && I == kKeyRow) prefetch(nxt);
+      v4f acc[kTiles][kChains];
+      {
+        const float4 tr = *reinterpret_cast<const float4 *>(adiag + I * 256 + l16 * 16 + 4 * q);
+        const float4 sc = *reinterpret_cast<const float4 *>(rsc + I * 16 + 4 * q);
+        const v8bf tp = split_bf16x4(make_float4(tr.x * sc.x, tr.y * sc.y, tr.z * sc.z, tr.w * sc.w));
+        const uint32_t(&r)[4][kWords] = rraw[I % (kDepth + 1)];
 #pragma unroll
         for (int tl = 0; tl < kTiles; ++tl) {
-          acc[tl][0][s] = sc * bf16_to_f32(rraw[I & 1][tl][s]);
+          const int w = tl >> 1;
+          // rows 0..3 of tile tl: the low or high halves of the row words
+          const uint32_t sel = tl & 1 ? 0x07060302u : 0x05040100u;
+          const uint32_t r01 = __builtin_amdgcn_perm(r[1][w], r[0][w], sel);
+          const uint32_t r23 = __builtin_amdgcn_perm(r[3][w], r[2][w], sel);
+          acc[tl][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tp, __builtin_bit_cast(v8bf, make_uint4(r01, r23, r01, r23)),
+                                                               v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
-          for (int c = 1; c < kChains; ++c) acc[tl][c][s] = 0.0f;
+          for (int c = 1; c < kChains; ++c) acc[tl][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
       }
 #pragma unroll
-      for (int J = 0; J < I; ++J) {
-        const uint2 ap = *reinterpret_cast<const uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q);
+      for (int pj = 0; pj < (I + 1) / 2; ++pj) {
+        const v8bf ap = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(smat + (pair_base(I) + pj) * 1024 + lane * 16));
 #pragma unroll
-        for (int tl = 0; tl < kTiles; ++tl)
-          acc[tl][J % kChains] =
-              __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, ap), xb[J][tl], acc[tl][J % kChains], 0, 0, 0);
+        for (int tl = 0; tl < kTiles; ++tl) {
+          const uint2 x0 = __builtin_bit_cast(uint2, xb[2 * pj][tl]);
+          const uint2 x1 = 2 * pj + 1 < I ? __builtin_bit_cast(uint2, xb[2 * pj + 1][tl]) : make_uint2(0u, 0u);
+          const int c = (pj + 1) % kChains;
+          acc[tl][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, __builtin_bit_cast(v8bf, make_uint4(x0.x, x0.y, x1.x, x1.y)),
+                                                               acc[tl][c], 0, 0, 0);
+        }
       }
-      const float4 tr = *reinterpret_cast<const float4 *>(adiag + I * 256 + l16 * 16 + 4 * q);
-      const float trv[4] = {tr.x, tr.y, tr.z, tr.w};
+      v4f xt[kTiles];
 #pragma unroll
       for (int tl = 0; tl < kTiles; ++tl) {
-        v4f sum = acc[tl][0];
+        v4f x = acc[tl][0];
 #pragma unroll
-        for (int c = 1; c < kChains; ++c) sum += acc[tl][c];
-        v4f x = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) x = __builtin_amdgcn_mfma_f32_16x16x4f32(trv[s], sum[s], x, 0, 0, 0);
-        const uint32_t p0 = f32_to_bf16(x[0]) | (f32_to_bf16(x[1]) << 16);
-        const uint32_t p1 = f32_to_bf16(x[2]) | (f32_to_bf16(x[3]) << 16);
+        for (int c = 1; c < kChains; ++c) x += acc[tl][c];
+        xt[tl] = x;
+        const uint32_t p0 = pack_bf16(x[0], x[1]);
+        const uint32_t p1 = pack_bf16(x[2], x[3]);
         xb[I][tl] = __builtin_bit_cast(v4s, make_uint2(p0, p1));
-        const uint32_t dcol = ((wave * kTiles + tl) & 7) * 16;
+      }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const uint32_t o = lbase + dcol + (I * 16 + s) * tstride;
-          if (a.out_f32)
-            of[o] = x[s];
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t o = lbase + (I * 16 + s) * tstride;
+        if constexpr (OUT_F32) {
+          if constexpr (kTiles == 2)
+            *(gptr<v2f>)(of + o) = v2f{xt[0][s], xt[1][s]};
           else
-            oh[o] = static_cast<uint16_t>(s < 2 ? (s == 0 ? p0 & 0xFFFFu : p0 >> 16) : (s == 2 ? p1 & 0xFFFFu : p1 >> 16));
+            *(gptr<v4f>)(of + o) = v4f{xt[0][s], xt[1][s], xt[2][s], xt[3][s]};
+        } else {
+          uint32_t wv[kWords];
+#pragma unroll
+          for (int j = 0; j < kWords; ++j)
+            wv[j] = static_cast<uint16_t>(xb[I][2 * j][s]) | (static_cast<uint32_t>(static_cast<uint16_t>(xb[I][2 * j + 1][s])) << 16);
+          if constexpr (kWords == 1)
+            *(gptr<uint32_t>)(oh + o) = wv[0];
+          else
+            *(gptr<v2u>)(oh + o) = v2u{wv[0], wv[1]};
         }
       }
     }
-    __syncthreads();  // LDS is rewritten by the next item
+    lds_barrier();  // every wave is done with this item's LDS contents
+    phase1();       // next item (an invalid one ends the loop; its phase 1 is harmless)
     cur = nxt;
   }
 }
 
-template <int NB>
+template <int NB, bool OUT_F32>
 __global__ __launch_bounds__(chunk_threads<NB>(), 1) void gdn_chunk_kernel(const ChunkArgs a, const int nitems) {
   constexpr int C = NB * 16;
   constexpr int kLowBlocks = NB * (NB - 1) / 2;
   __shared__ __attribute__((aligned(16))) uint8_t smat[C * 256];             // K^
   __shared__ __attribute__((aligned(16))) uint16_t ablk[(kLowBlocks > 0 ? kLowBlocks : 1) * 256];  // A_IJ, I > J
   __shared__ __attribute__((aligned(16))) float adiag[NB * 256];             // A_II, then T_II
-  __shared__ float gs[C], bs[C], rn[C], wsc[C], wsum[8];
-  chunk_items<NB>(a, nitems, smat, ablk, adiag, gs, bs, rn, wsc, wsum);
+  __shared__ float gs[C], bsw[2 * C], rn[C], wsum[8];  // bsw: beta, then W's row scales
+  chunk_items<NB, OUT_F32>(a, nitems, smat, ablk, adiag, gs, bsw, rn, bsw + C, wsum);
 }
 
-template <int NB>
+template <int NB, bool OUT_F32>
 qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
   const long long items = static_cast<long long>(a.B) * a.nchunks * a.H;  // (batch, chunk, head)
   if (items > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: too many chunks");
   if (items == 0) return QH_STATUS_OK;
-  // Persistent grid: as many workgroups as fit on the device at once.
-  static int slots[17] = {0};
+  // Persistent grid: as many workgroups as fit on the device at once (per device, cached).
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> slots[kMaxDevices];
   int dev = 0;
-  (void)hipGetDevice(&dev);
-  if (slots[NB] == 0) {
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  int grid_slots = dev >= 0 && dev < kMaxDevices ? slots[dev].load(std::memory_order_relaxed) : 0;
+  if (grid_slots == 0) {
     int per_cu = 0, cus = 0;
-    hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gdn_chunk_kernel<NB>, chunk_threads<NB>(), 0);
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gdn_chunk_kernel<NB, OUT_F32>, chunk_threads<NB>(), 0);
     if (err != hipSuccess) return hip_fail(err, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute");
-    slots[NB] = (per_cu < 1 ? 1 : per_cu) * cus;
+    grid_slots = (per_cu < 1 ? 1 : per_cu) * cus;
+    if (dev >= 0 && dev < kMaxDevices) slots[dev].store(grid_slots, std::memory_order_relaxed);
   }
-  long long grid = slots[NB];
-  if (grid > items) grid = items;
-  hipLaunchKernelGGL(gdn_chunk_kernel<NB>, dim3(static_cast<unsigned>(grid)), dim3(chunk_threads<NB>()), 0, stream, a,
-                     static_cast<int>(items));
-  const hipError_t err = hipGetLastError();
+  const long long grid = grid_slots < items ? grid_slots : items;
+  hipLaunchKernelGGL((gdn_chunk_kernel<NB, OUT_F32>), dim3(static_cast<unsigned>(grid)), dim3(chunk_threads<NB>()), 0,
+                     stream, a, static_cast<int>(items));
+  err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "gdn_chunk_kernel launch");
   return QH_STATUS_OK;
+}
+
+template <int NB>
+qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
+  return a.out_f32 ? launch_nb<NB, true>(a, stream) : launch_nb<NB, false>(a, stream);
 }
 
 }  // namespace
