@@ -31,10 +31,14 @@ namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int kD = 128;  // head dimension
+// Floats per diagonal 16 x 16 block in LDS: padded so that the four blocks a wave reads at once in
+// the diagonal inverses fall in different banks.
+constexpr int kDiagStride = 260;
 
 struct ChunkArgs {
   const uint16_t *k, *v;  // bf16 [B][T][H][D]
@@ -104,13 +108,19 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
   constexpr int kChains = kTiles >= 4 ? 1 : 4 / kTiles;
   static_assert(pair_base(NB) * 1024 <= C * 256, "A' pairs must fit in smat");
   constexpr int kRowPasses = C / (kChunkThreads / 8);   // K rows: 8 lanes per row
-  // Right-hand-side prefetch distance in block rows: deep enough that a row's loads (from HBM
-  // for the values) land before the substitution reaches it; all rows for C <= 128.
-  constexpr int kDepth = NB < 8 ? NB : 8;
+  // Right-hand-side loads (memory latency under this load is several microseconds): block rows
+  // [0, kEarly) are issued at the start of the item, under the A-build, the rest at the start of
+  // the substitution.
+  constexpr int kEarly = NB < 8 ? NB : 8;
   // Substitution row at whose start the next item's keys are prefetched (0: before the
   // diagonal inverses), once enough right-hand-side registers have been freed.
-  constexpr int kKeyRow = NB > kDepth ? kDepth : 0;
-  constexpr int kWords = kTiles / 2;                    // 32-bit words of a lane's right-hand-side row
+  constexpr int kKeyRow = NB >= 16 ? 12 : 0;
+  constexpr int kWords = kTiles / 2;  // 32-bit words per MFMA-layout row of a lane (16 kWords bytes row-major)
+  // Per-wave staging of right-hand-side and result rows (16 rows): in smat after the A' pairs
+  // when it fits, else in the A_IJ blocks (both free during the substitution).
+  constexpr int kStageRow = kWords == 1 ? 80 : 144;
+  constexpr bool kStageInSmat = pair_base(NB) * 1024 + kWaves * 16 * kStageRow <= C * 256;
+  static_assert(kStageInSmat || kWaves * 16 * kStageRow <= NB * (NB - 1) / 2 * 512, "staging must fit");
   static_assert(kRowPasses >= 1, "chunk too small for the workgroup");
   static_assert(kTiles == 2 || kTiles == 4, "tile pairing");
 
@@ -181,7 +191,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       ss += __shfl_xor(ss, 1, 64);
       ss += __shfl_xor(ss, 2, 64);
       ss += __shfl_xor(ss, 4, 64);
-      const float inv = 1.0f / sqrtf(ss + 1e-6f);
+      const float inv = rsqrtf(ss + 1e-6f);
       if (part == 0) rn[row] = inv;
       uint32_t o[8];
 #pragma unroll
@@ -210,6 +220,40 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
   phase1();
   while (cur.valid) {
     const int b = cur.b, h = cur.h, tok0 = cur.c * C;
+    // Right-hand sides.  A wave owns kTiles 16-column tiles, all of W (keys) or all of U
+    // (values): the 16 * kTiles adjacent columns from cb = ((wave * kTiles) % 8) * 16, column
+    // cb + kTiles * l16 + tl in tile tl; in the MFMA layout lane (q, l16) holds rows 4q .. 4q+3
+    // of its kTiles columns.  Global memory is accessed row-major instead, 16 rows x 32 kTiles
+    // bytes per block row and wave, 16 kWords bytes per lane (lane L: row L / 4, part L % 4),
+    // and transposed through a per-wave LDS staging area (rows kStageRow bytes apart: the four
+    // row groups of the MFMA layout fall in different banks).  Block rows [0, kEarly) load at
+    // the start of the item, under the A-build, the others when the substitution starts.  Byte offsets fit in 32 bits (B * T * H * 128 <= 2^31
+    // elements is checked at the boundary) and are added to base pointers held in SGPRs.
+    const bool is_w = wave * kTiles < 8;
+    const gptr<const uint8_t> rsrc = pick_ptr<const uint8_t>(is_w, a.k, a.v);
+    const uint32_t tstride = static_cast<uint32_t>(a.H) * kD;  // elements per token
+    const uint32_t tsb = 2 * tstride;                          // bytes per token
+    const int cb = ((wave * kTiles) & 7) * 16;
+    const uint32_t rm_base =
+        2 * ((static_cast<uint32_t>(b * a.T + tok0 + (lane >> 2)) * static_cast<uint32_t>(a.H) + h) * kD + cb) +
+        (lane & 3) * 16 * kWords;
+    uint8_t *const stg = (kStageInSmat ? smat + pair_base(NB) * 1024 : reinterpret_cast<uint8_t *>(ablk)) +
+                         wave * 16 * kStageRow;
+    uint8_t *const stg_rm = stg + (lane >> 2) * kStageRow + (lane & 3) * 16 * kWords;  // row-major slot
+    uint8_t *const stg_mf = stg + 4 * q * kStageRow + 4 * kWords * l16;               // MFMA-layout slot
+    // The running offset advances one block row at a time, opaque to the compiler, so that it
+    // does not precompute (and keep live) the offsets of every row.
+    uint32_t ld_off = rm_base;
+    v4u rring[NB][kWords];
+    auto rhs_load = [&](v4u (&r)[kWords]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int w = 0; w < kWords; ++w) r[w] = *(gptr<const v4u>)(rsrc + (ld_off + 16 * w));
+      ld_off += 16 * tsb;
+      asm volatile("" : "+v"(ld_off));
+    };
+#pragma unroll
+    for (int I = 0; I < kEarly; ++I) rhs_load(rring[I]);
+
     // ---- 2. A = -beta_i (K^ K^T)_ij e^{g_i - g_j}, lower blocks -----------------------------
     // Wave w < NB/2 takes the block rows I0 = w and I1 = NB-1-w (NB+1 blocks, balanced): the
     // key fragments of block row J (the MFMA B operand) are read once for both rows and
@@ -229,7 +273,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
         *reinterpret_cast<uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q) =
             make_uint2(pack_bf16(av[0], av[1]), pack_bf16(av[2], av[3]));
       } else {
-        *reinterpret_cast<float4 *>(adiag + I * 256 + l16 * 16 + 4 * q) = make_float4(av[0], av[1], av[2], av[3]);
+        *reinterpret_cast<float4 *>(adiag + I * kDiagStride + l16 * 16 + 4 * q) = make_float4(av[0], av[1], av[2], av[3]);
       }
     };
     auto frag = [&](int row_blk, int kk) __attribute__((always_inline)) {
@@ -274,33 +318,6 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     }
     lds_barrier();
 
-    // Right-hand sides.  A wave owns kTiles 16-column tiles, all of W (keys) or all of U
-    // (values): the 16 * kTiles adjacent columns from cb = ((wave * kTiles) % 8) * 16, column
-    // cb + kTiles * l16 + tl in tile tl, so that a lane reads (and writes) its kTiles columns of
-    // a row in one access; lane rows 4q .. 4q + 3 of a block row.  The first kDepth block rows
-    // load under the diagonal inverses.  Element offsets fit in 32 bits
-    // (B * T * H * 128 <= 2^31 is checked at the boundary).
-    const bool is_w = wave * kTiles < 8;
-    const gptr<const uint16_t> rsrc = pick_ptr<const uint16_t>(is_w, a.k, a.v);
-    const uint32_t tstride = static_cast<uint32_t>(a.H) * kD;  // elements per token
-    const uint32_t lbase = (static_cast<uint32_t>(b * a.T + tok0 + 4 * q) * static_cast<uint32_t>(a.H) + h) * kD +
-                           ((wave * kTiles) & 7) * 16 + kTiles * l16;
-    uint32_t rraw[kDepth + 1][4][kWords];
-    auto rhs_load = [&](int I, uint32_t (&r)[4][kWords]) __attribute__((always_inline)) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const gptr<const uint16_t> src = rsrc + lbase + (I * 16 + s) * tstride;
-        if constexpr (kWords == 1) {
-          r[s][0] = *(gptr<const uint32_t>)src;
-        } else {
-          const v2u v = *(gptr<const v2u>)src;
-          r[s][0] = v[0];
-          r[s][1] = v[1];
-        }
-      }
-    };
-#pragma unroll
-    for (int I = 0; I < kDepth && I < NB; ++I) rhs_load(I, rraw[I]);
     it += gridDim.x;
     const Item nxt = item_of(it);
     if (kKeyRow == 0) prefetch(nxt);
@@ -308,7 +325,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     // ---- 3. T_II = (I - A_II)^-1, one lane per column, in place ----------------------------
     if (t < NB * 16) {
       const int I = t >> 4, col = t & 15;  // the 16 lanes of a block are in one wave
-      const float *Ad = adiag + I * 256;
+      const float *Ad = adiag + I * kDiagStride;
       float x[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -318,7 +335,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
         x[r] = sacc;
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) adiag[I * 256 + r * 16 + col] = x[r];  // T_II row-major
+      for (int r = 0; r < 16; ++r) adiag[I * kDiagStride + r * 16 + col] = x[r];  // T_II row-major
     }
     lds_barrier();
 
@@ -332,14 +349,14 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     // (w, n) for n < w, else (NB-1-w, n-w); all A loads are issued first.
     if (wave < NB / 2) {
       const int I0 = wave, I1 = NB - 1 - wave;
-      const v8bf t0 = split_bf16x4(*reinterpret_cast<const float4 *>(adiag + I0 * 256 + l16 * 16 + 4 * q));
-      const v8bf t1 = split_bf16x4(*reinterpret_cast<const float4 *>(adiag + I1 * 256 + l16 * 16 + 4 * q));
+      const v8bf t0 = split_bf16x4(*reinterpret_cast<const float4 *>(adiag + I0 * kDiagStride + l16 * 16 + 4 * q));
+      const v8bf t1 = split_bf16x4(*reinterpret_cast<const float4 *>(adiag + I1 * kDiagStride + l16 * 16 + 4 * q));
       uint2 ac[NB - 1];
+      // block n of row I0 is ablk block I0(I0-1)/2 + n, of row I1 block I1(I1-1)/2 + n - I0
+      const uint16_t *const ab0 = ablk + (I0 * (I0 - 1) / 2) * 256 + l16 * 16 + 4 * q;
+      const uint16_t *const ab1 = ablk + (I1 * (I1 - 1) / 2 - I0) * 256 + l16 * 16 + 4 * q;
 #pragma unroll
-      for (int n = 0; n < NB - 1; ++n) {
-        const int I = n < I0 ? I0 : I1, J = n < I0 ? n : n - I0;
-        ac[n] = *reinterpret_cast<const uint2 *>(ablk + (I * (I - 1) / 2 + J) * 256 + l16 * 16 + 4 * q);
-      }
+      for (int n = 0; n < NB - 1; ++n) ac[n] = *reinterpret_cast<const uint2 *>((n < I0 ? ab0 : ab1) + n * 256);
 #pragma unroll
       for (int n = 0; n < NB - 1; ++n) {
         const int I = n < I0 ? I0 : I1, J = n < I0 ? n : n - I0;
@@ -359,18 +376,44 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     // per pair of blocks J for the sum; only the last pair depends on X_{I-1}.
     const float *const rsc = bs + (is_w ? C : 0);  // wsc = bs + C: one LDS object
     const gptr<float> of = pick_ptr<float>(is_w, a.w, a.u);
-    const gptr<uint16_t> oh = pick_ptr<uint16_t>(is_w, a.w, a.u);
+    const gptr<uint8_t> oh = pick_ptr<uint8_t>(is_w, a.w, a.u);
+    // fp32 outputs are stored from the MFMA layout (element offsets); bf16 through the staging
+    uint32_t st_off = OUT_F32 ? (static_cast<uint32_t>(b * a.T + tok0 + 4 * q) * static_cast<uint32_t>(a.H) + h) * kD +
+                                    cb + kTiles * l16
+                              : rm_base;
     v4s xb[NB][kTiles];  // X_J in bf16, the MFMA B-operand layout (= result layout)
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      if (I + kDepth < NB) rhs_load(I + kDepth, rraw[(I + kDepth) % (kDepth + 1)]);
+      if (I == 0) {
+#pragma unroll
+        for (int J = kEarly; J < NB; ++J) rhs_load(rring[J]);
+      }
       if (kKeyRow > 0 && I == kKeyRow) prefetch(nxt);
+      // this row's A' pairs, all reads issued before the T' operand is formed
+      uint4 apr[(NB + 1) / 2];
+#pragma unroll
+      for (int pj = 0; pj < (I + 1) / 2; ++pj)
+        apr[pj] = *reinterpret_cast<const uint4 *>(smat + (pair_base(I) + pj) * 1024 + lane * 16);
+      // right-hand side rows of block row I into the MFMA layout
+      uint32_t r[4][kWords];
+#pragma unroll
+      for (int w = 0; w < kWords; ++w)
+        *reinterpret_cast<v4u *>(stg_rm + 16 * w) = rring[I][w];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if constexpr (kWords == 1) {
+          r[s][0] = *reinterpret_cast<const uint32_t *>(stg_mf + s * kStageRow);
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2 *>(stg_mf + s * kStageRow);
+          r[s][0] = v.x;
+          r[s][1] = v.y;
+        }
+      }
       v4f acc[kTiles][kChains];
       {
-        const float4 tr = *reinterpret_cast<const float4 *>(adiag + I * 256 + l16 * 16 + 4 * q);
+        const float4 tr = *reinterpret_cast<const float4 *>(adiag + I * kDiagStride + l16 * 16 + 4 * q);
         const float4 sc = *reinterpret_cast<const float4 *>(rsc + I * 16 + 4 * q);
         const v8bf tp = split_bf16x4(make_float4(tr.x * sc.x, tr.y * sc.y, tr.z * sc.z, tr.w * sc.w));
-        const uint32_t(&r)[4][kWords] = rraw[I % (kDepth + 1)];
 #pragma unroll
         for (int tl = 0; tl < kTiles; ++tl) {
           const int w = tl >> 1;
@@ -386,7 +429,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
       }
 #pragma unroll
       for (int pj = 0; pj < (I + 1) / 2; ++pj) {
-        const v8bf ap = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4 *>(smat + (pair_base(I) + pj) * 1024 + lane * 16));
+        const v8bf ap = __builtin_bit_cast(v8bf, apr[pj]);
 #pragma unroll
         for (int tl = 0; tl < kTiles; ++tl) {
           const uint2 x0 = __builtin_bit_cast(uint2, xb[2 * pj][tl]);
@@ -403,29 +446,39 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
 #pragma unroll
         for (int c = 1; c < kChains; ++c) x += acc[tl][c];
         xt[tl] = x;
-        const uint32_t p0 = pack_bf16(x[0], x[1]);
-        const uint32_t p1 = pack_bf16(x[2], x[3]);
-        xb[I][tl] = __builtin_bit_cast(v4s, make_uint2(p0, p1));
+        xb[I][tl] = __builtin_bit_cast(v4s, make_uint2(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])));
       }
+      if constexpr (OUT_F32) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const uint32_t o = lbase + (I * 16 + s) * tstride;
-        if constexpr (OUT_F32) {
+        for (int s = 0; s < 4; ++s) {
+          const uint32_t o = st_off + s * tstride;
           if constexpr (kTiles == 2)
             *(gptr<v2f>)(of + o) = v2f{xt[0][s], xt[1][s]};
           else
             *(gptr<v4f>)(of + o) = v4f{xt[0][s], xt[1][s], xt[2][s], xt[3][s]};
-        } else {
+        }
+        st_off += 16 * tstride;
+      } else {
+        // X rows into the staging (MFMA layout), read back row-major, one wide store per lane
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
           uint32_t wv[kWords];
 #pragma unroll
-          for (int j = 0; j < kWords; ++j)
-            wv[j] = static_cast<uint16_t>(xb[I][2 * j][s]) | (static_cast<uint32_t>(static_cast<uint16_t>(xb[I][2 * j + 1][s])) << 16);
+          for (int j = 0; j < kWords; ++j) {
+            const v2u lo = __builtin_bit_cast(v2u, xb[I][2 * j]), hi = __builtin_bit_cast(v2u, xb[I][2 * j + 1]);
+            wv[j] = __builtin_amdgcn_perm(s < 2 ? hi[0] : hi[1], s < 2 ? lo[0] : lo[1], s & 1 ? 0x07060302u : 0x05040100u);
+          }
           if constexpr (kWords == 1)
-            *(gptr<uint32_t>)(oh + o) = wv[0];
+            *reinterpret_cast<uint32_t *>(stg_mf + s * kStageRow) = wv[0];
           else
-            *(gptr<v2u>)(oh + o) = v2u{wv[0], wv[1]};
+            *reinterpret_cast<uint2 *>(stg_mf + s * kStageRow) = make_uint2(wv[0], wv[1]);
         }
+#pragma unroll
+        for (int w = 0; w < kWords; ++w)
+          *(gptr<v4u>)(oh + (st_off + 16 * w)) = *reinterpret_cast<const v4u *>(stg_rm + 16 * w);
+        st_off += 16 * tsb;
       }
+      asm volatile("" : "+v"(st_off));
     }
     lds_barrier();  // every wave is done with this item's LDS contents
     phase1();       // next item (an invalid one ends the loop; its phase 1 is harmless)
@@ -439,7 +492,7 @@ __global__ __launch_bounds__(chunk_threads<NB>(), 1) void gdn_chunk_kernel(const
   constexpr int kLowBlocks = NB * (NB - 1) / 2;
   __shared__ __attribute__((aligned(16))) uint8_t smat[C * 256];             // K^
   __shared__ __attribute__((aligned(16))) uint16_t ablk[(kLowBlocks > 0 ? kLowBlocks : 1) * 256];  // A_IJ, I > J
-  __shared__ __attribute__((aligned(16))) float adiag[NB * 256];             // A_II, then T_II
+  __shared__ __attribute__((aligned(16))) float adiag[NB * kDiagStride];     // A_II, then T_II
   __shared__ float gs[C], bsw[2 * C], rn[C], wsum[8];  // bsw: beta, then W's row scales
   chunk_items<NB, OUT_F32>(a, nitems, smat, ablk, adiag, gs, bsw, rn, bsw + C, wsum);
 }
