@@ -109,8 +109,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
   static_assert(pair_base(NB) * 1024 <= C * 256, "A' pairs must fit in smat");
   constexpr int kRowPasses = C / (kChunkThreads / 8);   // K rows: 8 lanes per row
   // Right-hand-side loads (memory latency under this load is several microseconds): block rows
-  // [0, kEarly) are issued at the start of the item, under the A-build, the rest at the start of
-  // the substitution.
+  // [0, kEarly) are issued at the start of the item, under the A-build, the rest after it.
   constexpr int kEarly = NB < 8 ? NB : 8;
   // Substitution row at whose start the next item's keys are prefetched (0: before the
   // diagonal inverses), once enough right-hand-side registers have been freed.
@@ -227,7 +226,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     // bytes per block row and wave, 16 kWords bytes per lane (lane L: row L / 4, part L % 4),
     // and transposed through a per-wave LDS staging area (rows kStageRow bytes apart: the four
     // row groups of the MFMA layout fall in different banks).  Block rows [0, kEarly) load at
-    // the start of the item, under the A-build, the others when the substitution starts.  Byte offsets fit in 32 bits (B * T * H * 128 <= 2^31
+    // the start of the item, under the A-build, the others after it.  Byte offsets fit in 32 bits (B * T * H * 128 <= 2^31
     // elements is checked at the boundary) and are added to base pointers held in SGPRs.
     const bool is_w = wave * kTiles < 8;
     const gptr<const uint8_t> rsrc = pick_ptr<const uint8_t>(is_w, a.k, a.v);
@@ -318,6 +317,8 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     }
     lds_barrier();
 
+#pragma unroll
+    for (int J = kEarly; J < NB; ++J) rhs_load(rring[J]);  // the A-build's registers are free now
     it += gridDim.x;
     const Item nxt = item_of(it);
     if (kKeyRow == 0) prefetch(nxt);
@@ -384,10 +385,6 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
     v4s xb[NB][kTiles];  // X_J in bf16, the MFMA B-operand layout (= result layout)
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      if (I == 0) {
-#pragma unroll
-        for (int J = kEarly; J < NB; ++J) rhs_load(rring[J]);
-      }
       if (kKeyRow > 0 && I == kKeyRow) prefetch(nxt);
       // this row's A' pairs, all reads issued before the T' operand is formed
       uint4 apr[(NB + 1) / 2];
