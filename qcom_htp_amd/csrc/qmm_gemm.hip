@@ -632,8 +632,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   const int KC = K / 16;
   constexpr int P = 4;   // K chunks per lane in flight per output
   constexpr int EW = 1;  // outputs per wave in flight together
+  // Barriers here are LDS-only: waiting for the provisional stores (what __syncthreads' release
+  // fence does) is needed only before outputs are rewritten, i.e. only when there are marks.
+  bool stores_fenced = false;
   for (;;) {
-    __syncthreads();  // marks complete; provisional outputs stored before any rewrite
+    lds_read_barrier();  // marks complete
     uint32_t marks[kBlocks];
 #pragma unroll
     for (int b = 0; b < kBlocks; ++b) marks[b] = flagw[b * kGemmThreads + t];
@@ -657,9 +660,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
       }
       flagw[b * kGemmThreads + t] = keep;
     }
-    __syncthreads();
+    lds_read_barrier();
     const int total = fix_cnt;
     if (total == 0) break;
+    if (!stores_fenced) {
+      __syncthreads();  // every provisional output is stored before any is rewritten
+      stores_fenced = true;
+    }
     const int cnt = total < kFixCap ? total : kFixCap;
     for (int e0 = wave * EW; e0 < cnt; e0 += (kGemmThreads / 64) * EW) {
       // every per-output constant is requested together with the first operand chunks
@@ -753,7 +760,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
       }
     }
     if (total <= kFixCap) break;
-    __syncthreads();
+    lds_read_barrier();
     if (t == 0) fix_cnt = 0;
   }
 }
