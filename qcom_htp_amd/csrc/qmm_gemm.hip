@@ -56,6 +56,7 @@ struct GemmArgs {
   const int32_t *scale_exp;
   const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
+  const int8_t *resid;  // 8-bit acts: rounding residues [N][K]
   int M, N, K, KT, TM, TN;
   int act_zp, out_zp, out_qmax, out16;
   double sA, sO;
@@ -411,6 +412,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   __shared__ __attribute__((aligned(16))) uint8_t sA0[kTileA], sA1[kTileA];
   __shared__ __attribute__((aligned(16))) uint8_t sB0[C::kTileB], sB1[C::kTileB];
   __shared__ uint32_t fix_list[kFixCap];  // (row << 16 | column) inside the tile
+  // The exact integer sums of each listed output, taken from the accumulators: 8-bit acts
+  // S1 = sum (a - 128) w (int32); 16-bit acts X = sum (a - 32896) w and Y = sum (a - 32896) r.
+  __shared__ int64_t fix_val[MODE == 0 ? (A16 ? 2 * kFixCap : kFixCap / 2) : 1];
   __shared__ int fix_cnt;
   // Per-column epilogue constants of the tile, filled while the first operand tiles load.
   //   8-bit acts : [alpha | beta' | thr] x 256 columns;
@@ -499,11 +503,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // broadcasts + byte permutes) so every lane stores 4 adjacent outputs of one row.
   // Rounding: t + 1.5 * 2^52 leaves rint(t) in the low word (|t| < 2^30 is proven per
   // column at prepare time, otherwise t is clamped first).  A strip whose largest
-  // |t - rint(t)| exceeds the column's certified threshold takes a rare path that marks its
-  // uncertain outputs in LDS (in an operand stage every wave has finished reading; the marks
-  // must not stay in registers).  Marks: one dword per thread and 32x32 block, byte jg = strip
-  // jg, bit jj = row jj.  A mark is needed only if rint(t) lies in [0, qmax] (otherwise both
-  // candidate roundings clamp to the same output).
+  // |t - rint(t)| exceeds the column's certified threshold takes a rare path that lists its
+  // uncertain outputs in LDS together with their exact accumulator sums; beyond the list's
+  // capacity it marks them instead (in an operand stage every wave has finished reading: one
+  // dword per thread and 32x32 block, byte jg = strip jg, bit jj = row jj).  An output is
+  // uncertain only if rint(t) lies in [0, qmax] (otherwise both candidate roundings clamp to
+  // the same output).
   const int q = lane & 3;
   const double qmaxd = static_cast<double>(g.out_qmax);
   constexpr int kBlocks = A16 ? 2 : 4 * kNT;  // 32-row x 32-column output blocks per lane
@@ -565,15 +570,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             dmax = fmax(dmax, round_near<CLAMP>(tv, qmaxd, &oi));
             o[jj] = clamp_out(oi, g.out_qmax);
           });
-          if (dmax > thr) {  // rare: mark the uncertain outputs of the strip
-            uint32_t fm = 0;
-            static_for<4>([&](auto jj) {
-              const double tv = fma(static_cast<double>(acc[mt][nt][4 * decltype(jg)::value + decltype(jj)::value]), alpha, beta);
+          if (dmax > thr) {  // rare: list the uncertain outputs of the strip with their sums
+            uint32_t keep = 0;
+            static_for<4>([&](auto jjc) {
+              constexpr int j = 4 * decltype(jg)::value + decltype(jjc)::value;
+              const double tv = fma(static_cast<double>(acc[mt][nt][j]), alpha, beta);
               int oi;
               const double d = round_near<CLAMP>(tv, qmaxd, &oi);
-              fm |= static_cast<uint32_t>((d > thr) & (static_cast<uint32_t>(oi) <= static_cast<uint32_t>(g.out_qmax))) << jj;
+              const int r = R + decltype(jjc)::value;
+              if ((d > thr) & (static_cast<uint32_t>(oi) <= static_cast<uint32_t>(g.out_qmax)) && m0 + r < M && n0 + cl < g.N) {
+                const int slot = atomicAdd(&fix_cnt, 1);
+                if (slot < kFixCap) {
+                  fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(cl);
+                  reinterpret_cast<int32_t *>(fix_val)[slot] = acc[mt][nt][j];
+                } else {
+                  keep |= 1u << decltype(jjc)::value;  // beyond the list: a later pass
+                }
+              }
             });
-            flagb[((nt * 4 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(fm);
+            if (keep) flagb[((nt * 4 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(keep);
           }
           store_strip(g, tile_out, m0, n0, R + q, wn * 64 + nt * 32 + (lane & 28), o, q, full);
         });
@@ -603,14 +618,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             dmax = fmax(dmax, round_near<CLAMP>(t_of(jj), qmaxd, &oi));
             o[jj] = clamp_out(oi, g.out_qmax);
           });
-          if (dmax > thr) {  // rare: mark the uncertain outputs of the strip
-            uint32_t fm = 0;
-            static_for<4>([&](auto jj) {
+          if (dmax > thr) {  // rare: list the uncertain outputs of the strip with their sums
+            uint32_t keep = 0;
+            static_for<4>([&](auto jjc) {
+              constexpr int j = 4 * decltype(jg)::value + decltype(jjc)::value;
               int oi;
-              const double d = round_near<CLAMP>(t_of(jj), qmaxd, &oi);
-              fm |= static_cast<uint32_t>((d > thr) & (static_cast<uint32_t>(oi) <= static_cast<uint32_t>(g.out_qmax))) << jj;
+              const double d = round_near<CLAMP>(t_of(jjc), qmaxd, &oi);
+              const int r = R + decltype(jjc)::value;
+              if ((d > thr) & (static_cast<uint32_t>(oi) <= static_cast<uint32_t>(g.out_qmax)) && m0 + r < M && n0 + cl < g.N) {
+                const int slot = atomicAdd(&fix_cnt, 1);
+                if (slot < kFixCap) {
+                  fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(cl);
+                  fix_val[2 * slot] = 256 * static_cast<int64_t>(acc[2 * mt][2 * c][j]) + acc[2 * mt + 1][2 * c][j];
+                  fix_val[2 * slot + 1] = 256 * static_cast<int64_t>(acc[2 * mt][2 * c + 1][j]) + acc[2 * mt + 1][2 * c + 1][j];
+                } else {
+                  keep |= 1u << decltype(jjc)::value;  // beyond the list: a later pass
+                }
+              }
             });
-            flagb[((c * 2 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(fm);
+            if (keep) flagb[((c * 2 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(keep);
           }
           store_strip(g, tile_out, m0, n0, R + q, wn * 32 + (lane & 28), o, q, full);
         });
@@ -622,146 +648,207 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // With s32 = M * 2^E the oracle's weight is fl32(w * s32) = 2^E * W', W' = w * M + r for an
   // integer residue r, so the exact dot product is 2^E * D with
   //   D = sum_k (a_k - zp) W'_k = M * S1 + S2 + (base - zp) * (M * sum_k w_k + sum_k r_k),
-  //   S1 = sum_k (a_k - base) w_k,  S2 = sum_k (a_k - base) r_k   (base = 128 or 32768).
-  // Marked outputs are listed in passes of at most kFixCap.  Each wave takes whole outputs
-  // (EW at a time, P 16-deep K chunks per lane in flight), forms S1 and S2 exactly in integers
-  // and decides: t = D * sA * 2^E / sO + beta rounds like the oracle unless t is still within
-  // the oracle's own float64 noise of a boundary; those outputs get the float64 emulation of
-  // the oracle's dot product.
-  const int abase = A16 ? 32768 : 128;
+  //   S1 = sum_k (a_k - base) w_k,  S2 = sum_k (a_k - base) r_k.
+  // Marked outputs were listed by the epilogue with their accumulator sums: 8-bit acts S1
+  // (base 128); 16-bit acts S1 and S2 (base 32896, codes and residue columns).  Each wave takes
+  // whole outputs, forms S2 for 8-bit acts from the prepared residue plane (dot4 over K), and
+  // decides: t = D * sA * 2^E / sO + beta rounds like the oracle unless t is still within the
+  // oracle's own float64 noise of a boundary; those outputs get the float64 emulation of the
+  // oracle's dot product.  Marks beyond the list's capacity stay in the mark words and are
+  // handled in later passes that form S1 and S2 from the operands (base 128 or 32768).
   const int KC = K / 16;
-  constexpr int P = 4;   // K chunks per lane in flight per output
-  constexpr int EW = 1;  // outputs per wave in flight together
-  // Barriers here are LDS-only: waiting for the provisional stores (what __syncthreads' release
-  // fence does) is needed only before outputs are rewritten, i.e. only when there are marks.
-  bool stores_fenced = false;
-  for (;;) {
-    lds_read_barrier();  // marks complete
-    uint32_t marks[kBlocks];
-#pragma unroll
-    for (int b = 0; b < kBlocks; ++b) marks[b] = flagw[b * kGemmThreads + t];
-#pragma unroll
-    for (int b = 0; b < kBlocks; ++b) {
-      uint32_t mk = marks[b];
-      if (mk == 0) continue;
-      uint32_t keep = 0;
-      const int rb = A16 ? wm * 64 + (b & 1) * 32 + 4 * (lane >> 5) : wm * 128 + (b & 3) * 32 + 4 * (lane >> 5);
-      const int c = A16 ? wn * 32 + (lane & 31) : wn * 64 + (b >> 2) * 32 + (lane & 31);
-      while (mk) {
-        const int bit = __builtin_ctz(mk);
-        mk &= mk - 1;
-        const int r = rb + 8 * (bit >> 3) + (bit & 7);
-        if (m0 + r >= M || n0 + c >= g.N) continue;  // padding rows / columns of the tile
-        const int slot = atomicAdd(&fix_cnt, 1);
-        if (slot < kFixCap)
-          fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(c);
-        else
-          keep |= 1u << bit;  // listed in a later pass
-      }
-      flagw[b * kGemmThreads + t] = keep;
-    }
-    lds_read_barrier();
-    const int total = fix_cnt;
-    if (total == 0) break;
-    if (!stores_fenced) {
-      __syncthreads();  // every provisional output is stored before any is rewritten
-      stores_fenced = true;
-    }
-    const int cnt = total < kFixCap ? total : kFixCap;
-    for (int e0 = wave * EW; e0 < cnt; e0 += (kGemmThreads / 64) * EW) {
-      // every per-output constant is requested together with the first operand chunks
-      int mrow[EW], ncol[EW], mant[EW];
-      float mf[EW];
-      int64_t csq[EW], csr[EW];
-      double ae[EW], bt[EW], mx[EW], ab[EW];
-#pragma unroll
-      for (int i = 0; i < EW; ++i) {
-        const int e = e0 + i < cnt ? e0 + i : cnt - 1;
-        const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);  // uniform in the wave
-        mrow[i] = m0 + static_cast<int>(v >> 16);
-        const int n = n0 + static_cast<int>(v & 0xFFFFu);
-        ncol[i] = n;
-        mant[i] = static_cast<int>(g.mant[n]);
-        mf[i] = static_cast<float>(mant[i]);  // exact: M < 2^24
-        csq[i] = g.colsum[n];
-        csr[i] = g.colsum_r[n];
-        ae[i] = g.alpha_e[n];
-        bt[i] = g.beta[n];
-        mx[i] = g.margin_exact[n];
-        ab[i] = g.absb[n];
-      }
-      long long S1[EW], S2[EW];
-#pragma unroll
-      for (int i = 0; i < EW; ++i) S1[i] = S2[i] = 0;
-      for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
-        uint4 wr[EW][P];
-        uint4 av[EW][P][A16 ? 2 : 1];
-#pragma unroll
-        for (int i = 0; i < EW; ++i) {
+  constexpr int P = 4;  // 16-byte K chunks per lane in flight
+  lds_read_barrier();   // listed outputs and overflow marks complete
+  const int listed = fix_cnt;
+  if (listed > 0) {
+    __syncthreads();  // every provisional output is stored before any is rewritten
+    const int cnt = listed < kFixCap ? listed : kFixCap;
+    const int abase_acc = A16 ? 32896 : 128;
+    for (int e = wave; e < cnt; e += kGemmThreads / 64) {
+      const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);  // uniform in the wave
+      const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
+      long long S1, S2;
+      if (!A16) {
+        S1 = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int32_t *>(fix_val)[e]);
+        // S2 = sum_k (a_k - 128) r_k: 16 k per lane and chunk, 64 lanes x P chunks per round
+        const uint4 *const arow = reinterpret_cast<const uint4 *>(act + static_cast<size_t>(m) * K);
+        const uint4 *const rrow = reinterpret_cast<const uint4 *>(g.resid + static_cast<size_t>(n) * K);
+        int s2 = 0;  // |.| <= 128 * 64 * K < 2^31
+        for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
+          uint4 av[P], rv[P];
 #pragma unroll
           for (int pp = 0; pp < P; ++pp) {
             const int kc = kc0 + lane + 64 * pp;
-            const int k = kc < KC ? kc * 16 : 0;
-            const int n = ncol[i];
-            wr[i][pp] = load_w16_raw(g, A16 ? (n / 32) * 64 + (n % 32) : n, k);
-            const uint4 *ap = reinterpret_cast<const uint4 *>(act + (static_cast<size_t>(mrow[i]) * K + k) * (A16 ? 2 : 1));
-            av[i][pp][0] = ap[0];
-            if (A16) av[i][pp][A16 ? 1 : 0] = ap[1];
+            const int kk = kc < KC ? kc : 0;
+            av[pp] = arow[kk];
+            rv[pp] = rrow[kk];
           }
-        }
-#pragma unroll
-        for (int i = 0; i < EW; ++i) {
-          int s1 = 0, s2 = 0;  // |.| < 2^28 for P * 16 terms
 #pragma unroll
           for (int pp = 0; pp < P; ++pp) {
             if (kc0 + lane + 64 * pp >= KC) continue;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-              const int a = (A16 ? static_cast<int>(reinterpret_cast<const uint16_t *>(&av[i][pp][j >> 3])[j & 7])
-                                 : static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i][pp][0])[j])) - abase;
-              const int wj = w_at(wr[i][pp], j);
-              // W' = fl32(w * s32) / 2^E = fl32(w * M) (s32 = M * 2^E, no subnormals): the
-              // residue r = W' - w * M is minus the exact rounding error of that product
-              const float wf = static_cast<float>(wj);
-              const float prod = __fmul_rn(wf, mf[i]);
-              const int r = -static_cast<int>(__fmaf_rn(wf, mf[i], -prod));
-              s1 += __mul24(a, wj);
-              s2 += __mul24(a, r);
-            }
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].x ^ 0x80808080u), static_cast<int>(rv[pp].x), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].y ^ 0x80808080u), static_cast<int>(rv[pp].y), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].z ^ 0x80808080u), static_cast<int>(rv[pp].z), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].w ^ 0x80808080u), static_cast<int>(rv[pp].w), s2, false);
           }
-          S1[i] += s1;
-          S2[i] += s2;
         }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) s2 += __shfl_xor(s2, off, 64);
+        S2 = s2;
+      } else {
+        const long long x = fix_val[2 * e], y = fix_val[2 * e + 1];
+        S1 = static_cast<long long>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)))) |
+             (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32))) << 32);
+        S2 = static_cast<long long>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(y)))) |
+             (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(y >> 32))) << 32);
       }
-#pragma unroll
-      for (int i = 0; i < EW; ++i) {
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-          S1[i] += __shfl_xor(S1[i], off, 64);
-          S2[i] += __shfl_xor(S2[i], off, 64);
-        }
-        if (e0 + i >= cnt) continue;
-        const int m = mrow[i], n = ncol[i];
-        // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
-        const unsigned long long M64 = static_cast<unsigned long long>(static_cast<long long>(mant[i]));
-        const unsigned long long sw = M64 * static_cast<unsigned long long>(csq[i]) + static_cast<unsigned long long>(csr[i]);
-        const unsigned long long Du = M64 * static_cast<unsigned long long>(S1[i]) + static_cast<unsigned long long>(S2[i]) +
-                                      static_cast<unsigned long long>(static_cast<long long>(abase - g.act_zp)) * sw;
-        const double u = static_cast<double>(static_cast<long long>(Du)) * ae[i];
-        const double tv = u + bt[i];
-        const double rd = rint(tv);
-        const double slack = mx[i] + 0x1p-48 * (fabs(u) + fabs(tv) + ab[i]);
-        if (fabs(tv - rd) > 0.5 - slack) {
-          fixup_one<A16>(g, m, n, lane);
-        } else if (lane == 0) {
-          const int oi = static_cast<int>(rd);
-          store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
-        }
+      // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
+      const unsigned long long M64 = static_cast<unsigned long long>(static_cast<long long>(g.mant[n]));
+      const unsigned long long sw = M64 * static_cast<unsigned long long>(g.colsum[n]) + static_cast<unsigned long long>(g.colsum_r[n]);
+      const unsigned long long Du = M64 * static_cast<unsigned long long>(S1) + static_cast<unsigned long long>(S2) +
+                                    static_cast<unsigned long long>(static_cast<long long>(abase_acc - g.act_zp)) * sw;
+      const double u = static_cast<double>(static_cast<long long>(Du)) * g.alpha_e[n];
+      const double tv = u + g.beta[n];
+      const double rd = rint(tv);
+      const double slack = g.margin_exact[n] + 0x1p-48 * (fabs(u) + fabs(tv) + g.absb[n]);
+      if (fabs(tv - rd) > 0.5 - slack) {
+        fixup_one<A16>(g, m, n, lane);
+      } else if (lane == 0) {
+        const int oi = static_cast<int>(rd);
+        store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
       }
     }
-    if (total <= kFixCap) break;
-    lds_read_barrier();
-    if (t == 0) fix_cnt = 0;
+    if (listed > kFixCap) {
+      // overflow: the remaining marks, listed and recomputed from the operands pass by pass
+      lds_read_barrier();
+      if (t == 0) fix_cnt = 0;
+      const int abase = A16 ? 32768 : 128;
+      constexpr int EW = 1;  // outputs per wave in flight together
+      for (;;) {
+        lds_read_barrier();  // overflow marks complete
+        uint32_t marks[kBlocks];
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) marks[b] = flagw[b * kGemmThreads + t];
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+          uint32_t mk = marks[b];
+          if (mk == 0) continue;
+          uint32_t keep = 0;
+          const int rb = A16 ? wm * 64 + (b & 1) * 32 + 4 * (lane >> 5) : wm * 128 + (b & 3) * 32 + 4 * (lane >> 5);
+          const int c = A16 ? wn * 32 + (lane & 31) : wn * 64 + (b >> 2) * 32 + (lane & 31);
+          while (mk) {
+            const int bit = __builtin_ctz(mk);
+            mk &= mk - 1;
+            const int r = rb + 8 * (bit >> 3) + (bit & 7);
+            if (m0 + r >= M || n0 + c >= g.N) continue;  // padding rows / columns of the tile
+            const int slot = atomicAdd(&fix_cnt, 1);
+            if (slot < kFixCap)
+              fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(c);
+            else
+              keep |= 1u << bit;  // listed in a later pass
+          }
+          flagw[b * kGemmThreads + t] = keep;
+        }
+        lds_read_barrier();
+        const int total = fix_cnt;
+        if (total == 0) break;
+        const int cnt = total < kFixCap ? total : kFixCap;
+        for (int e0 = wave * EW; e0 < cnt; e0 += (kGemmThreads / 64) * EW) {
+          // every per-output constant is requested together with the first operand chunks
+          int mrow[EW], ncol[EW], mant[EW];
+          float mf[EW];
+          int64_t csq[EW], csr[EW];
+          double ae[EW], bt[EW], mx[EW], ab[EW];
+#pragma unroll
+          for (int i = 0; i < EW; ++i) {
+            const int e = e0 + i < cnt ? e0 + i : cnt - 1;
+            const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);  // uniform in the wave
+            mrow[i] = m0 + static_cast<int>(v >> 16);
+            const int n = n0 + static_cast<int>(v & 0xFFFFu);
+            ncol[i] = n;
+            mant[i] = static_cast<int>(g.mant[n]);
+            mf[i] = static_cast<float>(mant[i]);  // exact: M < 2^24
+            csq[i] = g.colsum[n];
+            csr[i] = g.colsum_r[n];
+            ae[i] = g.alpha_e[n];
+            bt[i] = g.beta[n];
+            mx[i] = g.margin_exact[n];
+            ab[i] = g.absb[n];
+          }
+          long long S1[EW], S2[EW];
+#pragma unroll
+          for (int i = 0; i < EW; ++i) S1[i] = S2[i] = 0;
+          for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
+            uint4 wr[EW][P];
+            uint4 av[EW][P][A16 ? 2 : 1];
+#pragma unroll
+            for (int i = 0; i < EW; ++i) {
+#pragma unroll
+              for (int pp = 0; pp < P; ++pp) {
+                const int kc = kc0 + lane + 64 * pp;
+                const int k = kc < KC ? kc * 16 : 0;
+                const int n = ncol[i];
+                wr[i][pp] = load_w16_raw(g, A16 ? (n / 32) * 64 + (n % 32) : n, k);
+                const uint4 *ap = reinterpret_cast<const uint4 *>(act + (static_cast<size_t>(mrow[i]) * K + k) * (A16 ? 2 : 1));
+                av[i][pp][0] = ap[0];
+                if (A16) av[i][pp][A16 ? 1 : 0] = ap[1];
+              }
+            }
+#pragma unroll
+            for (int i = 0; i < EW; ++i) {
+              int s1 = 0, s2 = 0;  // |.| < 2^28 for P * 16 terms
+#pragma unroll
+              for (int pp = 0; pp < P; ++pp) {
+                if (kc0 + lane + 64 * pp >= KC) continue;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                  const int a = (A16 ? static_cast<int>(reinterpret_cast<const uint16_t *>(&av[i][pp][j >> 3])[j & 7])
+                                     : static_cast<int>(reinterpret_cast<const uint8_t *>(&av[i][pp][0])[j])) - abase;
+                  const int wj = w_at(wr[i][pp], j);
+                  // W' = fl32(w * s32) / 2^E = fl32(w * M) (s32 = M * 2^E, no subnormals): the
+                  // residue r = W' - w * M is minus the exact rounding error of that product
+                  const float wf = static_cast<float>(wj);
+                  const float prod = __fmul_rn(wf, mf[i]);
+                  const int r = -static_cast<int>(__fmaf_rn(wf, mf[i], -prod));
+                  s1 += __mul24(a, wj);
+                  s2 += __mul24(a, r);
+                }
+              }
+              S1[i] += s1;
+              S2[i] += s2;
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < EW; ++i) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+              S1[i] += __shfl_xor(S1[i], off, 64);
+              S2[i] += __shfl_xor(S2[i], off, 64);
+            }
+            if (e0 + i >= cnt) continue;
+            const int m = mrow[i], n = ncol[i];
+            // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
+            const unsigned long long M64 = static_cast<unsigned long long>(static_cast<long long>(mant[i]));
+            const unsigned long long sw = M64 * static_cast<unsigned long long>(csq[i]) + static_cast<unsigned long long>(csr[i]);
+            const unsigned long long Du = M64 * static_cast<unsigned long long>(S1[i]) + static_cast<unsigned long long>(S2[i]) +
+                                          static_cast<unsigned long long>(static_cast<long long>(abase - g.act_zp)) * sw;
+            const double u = static_cast<double>(static_cast<long long>(Du)) * ae[i];
+            const double tv = u + bt[i];
+            const double rd = rint(tv);
+            const double slack = mx[i] + 0x1p-48 * (fabs(u) + fabs(tv) + ab[i]);
+            if (fabs(tv - rd) > 0.5 - slack) {
+              fixup_one<A16>(g, m, n, lane);
+            } else if (lane == 0) {
+              const int oi = static_cast<int>(rd);
+              store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
+            }
+          }
+        }
+        if (total <= kFixCap) break;
+        lds_read_barrier();
+        if (t == 0) fix_cnt = 0;
+      }
+    }
   }
 }
 
@@ -798,6 +885,7 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.scale_exp = D.scale_exp;
   g.margin_exact = D.margin_exact;
   g.s32 = D.s32;
+  g.resid = D.resid;
   g.M = m;
   g.N = sh.N;
   g.K = sh.K;

@@ -80,6 +80,8 @@ struct QmmDevice {
   int32_t *scale_exp; // E of s32 = M * 2^E
   double *margin_exact; // 8-bit acts: float64 noise bound of the oracle's dot product, output LSB
   double *gemv_margin_r1; // 16-bit acts GEMV: per-channel coefficient of R1[m] in the margin
+  int8_t *resid;    // 8-bit acts: rounding residues r[n][k] (fl32(w s32) = 2^E (w M + r)), [N][K],
+                    // read by the GEMM's exact fixup (|r| <= 64)
 };
 
 struct QmmShape {

@@ -316,6 +316,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.scale_exp, scale_exp);
   if (st == QH_STATUS_OK) st = al.upload(&D.margin_exact, margin_exact);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
+  if (st == QH_STATUS_OK && !a16) st = al.upload(&D.resid, resid);
   if (st != QH_STATUS_OK) {
     al.release();
     delete p;
