@@ -84,8 +84,21 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-__device__ __forceinline__ void load_lds16(const void *gsrc, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((gbl_void_ptr)(const_cast<void *>(gsrc)), (lds_void_ptr)(lds_wave_base), 16, 0, 0);
+// 16 bytes per lane from global memory (base + off, base uniform) straight into LDS (lane i
+// writes lds_wave_base + 16 i).  ASM: issued from inline assembly, invisible to the compiler's
+// wait-count bookkeeping.  The builtin form makes the compiler treat every fragment read issued
+// while such a load is in flight as needing lgkmcnt(0); the k loop accounts for its own loads
+// with explicit vmcnt waits (and a barrier before a stage is rewritten), so it uses the
+// assembly form, and the kernel waits for vmcnt(0) itself before the operand stages are reused
+// or the waves end.
+template <bool ASM>
+__device__ __forceinline__ void load_lds16(const uint8_t *base, uint32_t off, void *lds_wave_base) {
+  if (ASM) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave_base)));
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0v), "v"(off), "s"(base) : "memory");
+  } else {
+    __builtin_amdgcn_global_load_lds((gbl_void_ptr)(const_cast<uint8_t *>(base + off)), (lds_void_ptr)(lds_wave_base), 16, 0, 0);
+  }
 }
 
 __device__ __forceinline__ void store_out(void *out, int out16, size_t idx, int v) {
@@ -243,32 +256,35 @@ struct MainCtx {
 };
 
 // Issue the direct-to-LDS loads of k-tile kt into the stage (wa, wb).
-template <bool A16>
+template <bool A16, bool ASM>
 __device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__restrict__ wa, uint8_t *__restrict__ wb) {
   using C = Cfg;
+  // 32-bit byte offsets from uniform bases: the tile's first activation row, the k-tile of
+  // the weight panel (256 rows x K x 2 bytes < 2^32 for K < 2^23)
+  const uint8_t *const abase = c.act + static_cast<size_t>(c.m0) * c.K * (A16 ? 2 : 1);
 #pragma unroll
   for (int j = 0; j < C::kLoadsA; ++j) {
     const int slot = j * kGemmThreads + c.t;  // 16-byte slot of the tile
-    const void *src;
+    uint32_t off;
     if (!A16) {
       const int row = slot >> 3, phys = slot & 7;
       const int logical = phys ^ swz8(row);
-      const int m = c.m0 + row < c.M ? c.m0 + row : c.M - 1;
+      const int r = c.m0 + row < c.M ? row : c.M - 1 - c.m0;
       const int k = kt * kBK + 16 * logical < c.K ? kt * kBK + 16 * logical : c.K - 16;
-      src = c.act + static_cast<size_t>(m) * c.K + k;
+      off = static_cast<uint32_t>(r) * static_cast<uint32_t>(c.K) + static_cast<uint32_t>(k);
     } else {
       const int row = slot >> 4, phys = slot & 15;
       const int logical = phys ^ swz16(row);
-      const int m = c.m0 + row < c.M ? c.m0 + row : c.M - 1;
+      const int r = c.m0 + row < c.M ? row : c.M - 1 - c.m0;
       const int k = kt * kBK + 8 * logical < c.K ? kt * kBK + 8 * logical : c.K - 8;
-      src = c.act + (static_cast<size_t>(m) * c.K + k) * 2;
+      off = (static_cast<uint32_t>(r) * static_cast<uint32_t>(c.K) + static_cast<uint32_t>(k)) * 2u;
     }
-    load_lds16(src, wa + (j * kGemmThreads + c.wave * 64) * 16);
+    load_lds16<ASM>(abase, off, wa + (j * kGemmThreads + c.wave * 64) * 16);
   }
   const uint8_t *bsrc = c.btiles + static_cast<size_t>(kt) * C::kTileB;
 #pragma unroll
   for (int j = 0; j < C::kLoadsB; ++j)
-    load_lds16(bsrc + (j * kGemmThreads + c.t) * 16, wb + (j * kGemmThreads + c.wave * 64) * 16);
+    load_lds16<ASM>(bsrc, static_cast<uint32_t>(j * kGemmThreads + c.t) * 16u, wb + (j * kGemmThreads + c.wave * 64) * 16);
 }
 
 // Raw LDS words of one 32-k step: A fragments and B fragments.
@@ -371,7 +387,7 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
       // The issue is not behind a branch, so its loads interleave with the MFMAs below.
       wait_tiles<C::kLoads>(S - 2);
       lds_read_barrier();
-      issue_tile<A16>(c, min(kt + S, KT - 1), la, lb);
+      issue_tile<A16, true>(c, min(kt + S, KT - 1), la, lb);
     }
     // LDS words of step sigma + 2 (tile kt step kk + 2, or tile kt + 1 step kk - 2)
     if (kk < 2)
@@ -457,7 +473,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     ccorr = g.corr[cn];
     if (A16) cmant = g.mant[cn];
   }
-  static_for<S>([&](auto p) { issue_tile<A16>(mc, min(static_cast<int>(p), KT - 1), stage_a(p), stage_b(p)); });
+  static_for<S>([&](auto p) { issue_tile<A16, false>(mc, min(static_cast<int>(p), KT - 1), stage_a(p), stage_b(p)); });
   if (MODE == 0) {
     const double alpha = cv[0];
     // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
@@ -494,9 +510,28 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     k_tile<A16>(mc, kt, KT, stage_a(sc), stage_b(sc), stage_a(std::integral_constant<int, ns>{}),
                 stage_b(std::integral_constant<int, ns>{}), pr, acc);
   };
-  for (int kt0 = 0; kt0 < KT; kt0 += S) static_for<S>([&](auto sc) {
-      if (kt0 + sc < KT) tile(kt0 + sc, sc);
-    });
+  // 8-bit acts: tile 0 runs first on its own; it waits for the prologue's loads (the only ones
+  // the compiler knows of), so none of those is in flight in the loop.  (16-bit acts keep
+  // tile 0 in the loop: their registers do not allow the extra copy.)  The loop body is
+  // branch-free (whole tile pairs), so the compiler's wait counts for the fragment reads stay
+  // exact across iterations; an odd last tile runs after it.
+  if (!A16) {
+    tile(0, std::integral_constant<int, 0>{});
+    int kt0 = 1;
+    for (; kt0 + S <= KT; kt0 += S) {
+      tile(kt0, std::integral_constant<int, 1>{});
+      tile(kt0 + 1, std::integral_constant<int, 0>{});
+    }
+    if (kt0 < KT) tile(kt0, std::integral_constant<int, 1>{});
+  } else {
+    int kt0 = 0;
+    for (; kt0 + S <= KT; kt0 += S) {
+      tile(kt0, std::integral_constant<int, 0>{});
+      tile(kt0 + 1, std::integral_constant<int, 1>{});
+    }
+    if (kt0 < KT) tile(kt0, std::integral_constant<int, 0>{});
+  }
+  wait_vmcnt<0>();  // the tile loads issued from assembly have landed
   // ---------------------------------------------------------------- epilogue
   // Straight from the accumulator registers: each lane requantises the 4-row strips of its
   // MFMA blocks (one column), then the 4 lanes of a quad transpose their strips (DPP quad
