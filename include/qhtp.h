@@ -128,6 +128,54 @@ qh_status qh_qmm_query(const qh_qmm_prepared *prep, qh_qmm_info *info);
 /* Frees the prepared state (synchronises the device first). NULL is accepted. */
 qh_status qh_qmm_release(qh_qmm_prepared *prep);
 
+/* Packed weight carriers of the reference: the byte streams its graph generator writes
+ * (example/qnn_hmx_matmul_common/gen_quant_chain.py, pack orders of --w8-pack-order /
+ * --w4-pack-order) and its op packages read.  K is the reduction depth, N the output channels;
+ * "[R, C]" is the carrier tensor's trailing shape, stored row-major. */
+typedef enum qh_weight_carrier {
+  QH_CARRIER_I8_KN = 0,            /* [K, N] int8, logical order ("raw", gen_quant_chain.py:729-738)      */
+  QH_CARRIER_W8_KMAJOR = 1,        /* [K, N] bytes: 32x32 K-major HMX tiles in (k tile, n tile) order,     */
+                                   /* element (r, c) at (r/4)*128 + c*4 + r%4 (gen_quant_chain.py:285-303; */
+                                   /* the output of HmxW4LpbqExpandToI8, HmxW4LpbqExpandToI8Op.cpp:84-101)  */
+  QH_CARRIER_W8_KMAJOR_SPLIT128 = 2, /* one W8_KMAJOR stream per 128 channels (gen_quant_chain.py:306-314) */
+  QH_CARRIER_W4_KMAJOR_N64 = 3,    /* [K, N/2]: 32x64 tiles of 1024 B, byte kg*128 + (n%32)*4 + kr holds   */
+                                   /* channels n (low) and n+32 (high) of one k; the stream               */
+                                   /* HmxU8I4ToU8MatMul reads (HmxU8I4ToU8MatMulOp.cpp:184-201)           */
+  QH_CARRIER_W4_KPAIR = 4,         /* [K/2, N]: byte (k/2, n), even k low (HmxW4LpbqExpandToI8Op.cpp:35-41) */
+  QH_CARRIER_W4_NMAJOR_KPAIR = 5,  /* the K-pair bytes in [N][K/2] memory order (gen_quant_chain.py:385-398) */
+  QH_CARRIER_W4_NMAJOR_K4 = 6,     /* N32 tiles, then 8-k groups of k / k+4 pairs (gen_quant_chain.py:401-422) */
+  QH_CARRIER_W4_KBLOCK32_NMAJOR_K4 = 7, /* 32-k blocks, then N32 tiles of k / k+4 pairs; the stream      */
+                                   /* HmxU16I4ToU16MatMul reads (HmxU16I4ToU16MatMulOp.cpp:526-543)       */
+  QH_CARRIER_W4_NPAIR_NMAJOR = 8,  /* [N/2, K]: channels n (even, low) and n+1 (gen_quant_chain.py:455-468) */
+  QH_CARRIER_W4_NPAIR_TILE32_NMAJOR = 9, /* [N/2, K]: channels n and n+32 per 64 (gen_quant_chain.py:471-489) */
+  QH_CARRIER_W4_FULL_CODES = 10,   /* [K, N]: one 4-bit code per byte (gen_quant_chain.py:619-627)          */
+} qh_weight_carrier;
+
+enum {
+  QH_CARRIER_XOR80 = 1u,  /* every byte stored with its sign bit toggled (the DLC carrier form,  */
+                          /* gen_quant_chain.py:645,676,716,738)                                  */
+  QH_CARRIER_HILO = 2u,   /* W4: the first element of a pair in the high nibble ("_hilo" orders) */
+  QH_CARRIER_BIASED = 4u, /* W4: nibble = code + 8 instead of two's complement                   */
+};
+
+/* Decodes a carrier into logical int8 codes weight_nk[N][K] (the layout qh_qmm_desc takes).
+ * Host memory in and out; no device work.  packed_bytes must equal the carrier's size
+ * (K*N for W8 carriers and W4_FULL_CODES, K*N/2 for the other W4 carriers).  Shape rules of
+ * the generator apply (K, N multiples of 32; N multiple of 64 / 128 where the layout tiles N
+ * by 64 / 128).  Replaces the per-element readers of the op packages
+ * (HmxU8I4ToU8MatMulOp.cpp:178-201, HmxU16I4ToU16MatMulOp.cpp:514-543) and the prepare-time
+ * unpacking they imply. */
+qh_status qh_weight_unpack(uint32_t carrier, uint32_t flags, const uint8_t *packed, size_t packed_bytes, uint32_t k,
+                           uint32_t n, int8_t *weight_nk);
+
+/* The HmxW4LpbqExpandToI8 op on device memory (HmxW4LpbqExpandToI8Op.cpp:47-104):
+ * weight_lpbq_dev [K/2, N] K-pair int4 bytes (QH_CARRIER_W4_KPAIR), block_scale_dev
+ * [N * K/32] uint8 integer scales (index n * K/32 + k/32) ->
+ * expanded_dev [K, N] bytes = sat_i8(q4 * scale) in the QH_CARRIER_W8_KMAJOR stream.
+ * K % 32 == 0, N % 32 == 0.  Stream-ordered, allocates nothing. */
+qh_status qh_w4_lpbq_expand_to_i8(const uint8_t *weight_lpbq_dev, const uint8_t *block_scale_dev,
+                                  uint8_t *expanded_dev, uint32_t k, uint32_t n, void *stream);
+
 /* ------------------------------------------------------------------------------------ */
 /* GDN / KDA triangular solve  T = (I - A)^-1, A strictly lower triangular per head      */
 /* ------------------------------------------------------------------------------------ */

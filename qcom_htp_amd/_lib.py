@@ -22,6 +22,24 @@ QH_WEIGHT_I8 = 0
 QH_WEIGHT_I4 = 1
 QH_WEIGHT_I4_LPBQ = 2
 
+# Packed weight carriers (qh_weight_carrier) and their flags.
+CARRIERS = {
+    "i8_kn": 0,
+    "w8_kmajor": 1,
+    "w8_kmajor_split128": 2,
+    "w4_kmajor_n64": 3,
+    "w4_kpair": 4,
+    "w4_nmajor_kpair": 5,
+    "w4_nmajor_k4": 6,
+    "w4_kblock32_nmajor_k4": 7,
+    "w4_npair_nmajor": 8,
+    "w4_npair_tile32_nmajor": 9,
+    "w4_full_codes": 10,
+}
+QH_CARRIER_XOR80 = 1
+QH_CARRIER_HILO = 2
+QH_CARRIER_BIASED = 4
+
 QH_GDN_FP32 = 0
 QH_GDN_BF16 = 1
 
@@ -39,6 +57,8 @@ EXPORTED = (
     "qh_qmm_accumulate",
     "qh_qmm_query",
     "qh_qmm_release",
+    "qh_weight_unpack",
+    "qh_w4_lpbq_expand_to_i8",
     "qh_gdn_solve_f32",
     "qh_gdn_solve_u16",
     "qh_gdn_chunk_uw",
@@ -114,6 +134,10 @@ def _declare(L: C.CDLL) -> None:
     L.qh_qmm_query.restype = st
     L.qh_qmm_release.argtypes = [vp]
     L.qh_qmm_release.restype = st
+    L.qh_weight_unpack.argtypes = [u32, u32, vp, C.c_size_t, u32, u32, vp]
+    L.qh_weight_unpack.restype = st
+    L.qh_w4_lpbq_expand_to_i8.argtypes = [vp, vp, vp, u32, u32, vp]
+    L.qh_w4_lpbq_expand_to_i8.restype = st
     L.qh_gdn_solve_f32.argtypes = [vp, vp, u32, u32, u32, vp]
     L.qh_gdn_solve_f32.restype = st
     L.qh_gdn_solve_u16.argtypes = [vp, vp, u32, u32, i32, i32, f32, f32, u32, vp]

@@ -119,6 +119,18 @@ qh_status qh_qmm_release(qh_qmm_prepared *prep) {
   return QH_STATUS_OK;
 }
 
+qh_status qh_w4_lpbq_expand_to_i8(const uint8_t *weight_lpbq_dev, const uint8_t *block_scale_dev,
+                                  uint8_t *expanded_dev, uint32_t k, uint32_t n, void *stream) {
+  if (!weight_lpbq_dev || !block_scale_dev || !expanded_dev)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_w4_lpbq_expand_to_i8: NULL buffer");
+  if (k == 0 || n == 0 || k % 32 || n % 32 || k > (1u << 20) || n > (1u << 20))
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_w4_lpbq_expand_to_i8: K=%u N=%u (need multiples of 32, <= 2^20)", k, n);
+  if (reinterpret_cast<uintptr_t>(weight_lpbq_dev) % 4 || reinterpret_cast<uintptr_t>(expanded_dev) % 16)
+    return fail(QH_STATUS_INVALID_ARGUMENT,
+                "qh_w4_lpbq_expand_to_i8: codes must be 4-byte and the output 16-byte aligned");
+  return launch_lpbq_expand(weight_lpbq_dev, block_scale_dev, expanded_dev, k, n, static_cast<hipStream_t>(stream));
+}
+
 qh_status qh_gdn_solve_f32(const float *A_dev, float *T_dev, uint32_t heads, uint32_t C, uint32_t precision,
                            void *stream) {
   if (A_dev == nullptr || T_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_f32: NULL buffer");
