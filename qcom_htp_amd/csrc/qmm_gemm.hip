@@ -155,6 +155,17 @@ __device__ __forceinline__ void store_strip(const GemmArgs &g, uint8_t *tile_out
   }
 }
 
+// Sum over the 64 lanes of a wave: DPP adds within each row of 16 lanes (quad swaps, then the
+// half-row and row mirrors), then the four row sums from lanes 0, 16, 32, 48.
+__device__ __forceinline__ int wave_sum(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm [1, 0, 3, 2]
+  v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm [2, 3, 0, 1]
+  v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);  // row_mirror
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+         __builtin_amdgcn_readlane(v, 48);
+}
+
 __device__ __forceinline__ int clamp_out(int v, int qmax) { return min(max(v, 0), qmax); }
 
 // rint(t) without the float64 round / convert instructions: adding 1.5 * 2^52 leaves the
@@ -702,10 +713,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     for (int e = wave; e < cnt; e += kGemmThreads / 64) {
       const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);  // uniform in the wave
       const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
+      // the column's constants are requested first, so their loads overlap the operand rows'.
+      // The index goes through a vector register: as wave-uniform values the compiler would
+      // move them to scalar registers at once, which waits for the loads before the rows issue.
+      int nv = n;
+      asm volatile("" : "+v"(nv));
+      const long long mant_n = g.mant[nv], csum_n = g.colsum[nv], csum_r_n = g.colsum_r[nv];
+      const double alpha_e_n = g.alpha_e[nv], beta_n = g.beta[nv], margin_n = g.margin_exact[nv], absb_n = g.absb[nv];
       long long S1, S2;
       if (!A16) {
         S1 = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int32_t *>(fix_val)[e]);
-        // S2 = sum_k (a_k - 128) r_k: 16 k per lane and chunk, 64 lanes x P chunks per round
+        // S2 = sum_k (a_k - 128) r_k: 16 k per lane and chunk, 64 lanes x P chunks per round;
+        // chunks past K read chunk 0 and count as zero residues (no branch in the round)
         const uint4 *const arow = reinterpret_cast<const uint4 *>(act + static_cast<size_t>(m) * K);
         const uint4 *const rrow = reinterpret_cast<const uint4 *>(g.resid + static_cast<size_t>(n) * K);
         int s2 = 0;  // |.| <= 128 * 64 * K < 2^31
@@ -720,16 +739,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
           }
 #pragma unroll
           for (int pp = 0; pp < P; ++pp) {
-            if (kc0 + lane + 64 * pp >= KC) continue;
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].x ^ 0x80808080u), static_cast<int>(rv[pp].x), s2, false);
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].y ^ 0x80808080u), static_cast<int>(rv[pp].y), s2, false);
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].z ^ 0x80808080u), static_cast<int>(rv[pp].z), s2, false);
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].w ^ 0x80808080u), static_cast<int>(rv[pp].w), s2, false);
+            const uint32_t keep = kc0 + lane + 64 * pp < KC ? 0xFFFFFFFFu : 0u;
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].x ^ 0x80808080u), static_cast<int>(rv[pp].x & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].y ^ 0x80808080u), static_cast<int>(rv[pp].y & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].z ^ 0x80808080u), static_cast<int>(rv[pp].z & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].w ^ 0x80808080u), static_cast<int>(rv[pp].w & keep), s2, false);
           }
         }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) s2 += __shfl_xor(s2, off, 64);
-        S2 = s2;
+        S2 = wave_sum(s2);
       } else {
         const long long x = fix_val[2 * e], y = fix_val[2 * e + 1];
         S1 = static_cast<long long>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(x)))) |
@@ -738,14 +755,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
              (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(y >> 32))) << 32);
       }
       // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
-      const unsigned long long M64 = static_cast<unsigned long long>(static_cast<long long>(g.mant[n]));
-      const unsigned long long sw = M64 * static_cast<unsigned long long>(g.colsum[n]) + static_cast<unsigned long long>(g.colsum_r[n]);
+      const unsigned long long M64 = static_cast<unsigned long long>(mant_n);
+      const unsigned long long sw = M64 * static_cast<unsigned long long>(csum_n) + static_cast<unsigned long long>(csum_r_n);
       const unsigned long long Du = M64 * static_cast<unsigned long long>(S1) + static_cast<unsigned long long>(S2) +
                                     static_cast<unsigned long long>(static_cast<long long>(abase_acc - g.act_zp)) * sw;
-      const double u = static_cast<double>(static_cast<long long>(Du)) * g.alpha_e[n];
-      const double tv = u + g.beta[n];
+      const double u = static_cast<double>(static_cast<long long>(Du)) * alpha_e_n;
+      const double tv = u + beta_n;
       const double rd = rint(tv);
-      const double slack = g.margin_exact[n] + 0x1p-48 * (fabs(u) + fabs(tv) + g.absb[n]);
+      const double slack = margin_n + 0x1p-48 * (fabs(u) + fabs(tv) + absb_n);
       if (fabs(tv - rd) > 0.5 - slack) {
         fixup_one<A16>(g, m, n, lane);
       } else if (lane == 0) {
