@@ -231,6 +231,24 @@ def measured_traffic(kernel_key: str):
         return None
 
 
+def lpbq_expand_workload(k: int, n: int, steps: int, warmup: int):
+    """HmxW4LpbqExpandToI8 on the device: [K/2, N] int4 K-pair codes + [N * K/32] scales -> [K, N]
+    int8 K-major tiles.  Byte work: K*N/2 + N*K/32 bytes in, K*N bytes out."""
+    import torch
+
+    from qcom_htp_amd.ops import HmxW4LpbqExpandToI8
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    codes = torch.randint(0, 256, (1, 1, k // 2, n), dtype=torch.uint8, device=dev, generator=gen)
+    scales = torch.randint(1, 16, (1, 1, 1, n * (k // 32)), dtype=torch.uint8, device=dev, generator=gen)
+    out = torch.empty((1, 1, k, n), dtype=torch.uint8, device=dev)
+    wall, ev = time_kernel(lambda i: HmxW4LpbqExpandToI8(codes, scales, out=out), steps, warmup)
+    nbytes = k * n // 2 + n * (k // 32) + k * n
+    return {"k": k, "n": n, "ms": ev, "wall_ms": wall, "bytes": nbytes, "gbs": nbytes / (ev * 1e-3) / 1e9}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -274,6 +292,7 @@ def main() -> int:
             jobs.append((f"gdn_c256_h32_{'fp32' if prec == 0 else 'bf16'}", lambda prec=prec: gdn_workload(32, 256, 50, 5, prec)))
         for C in (64, 256):
             jobs.append((f"gdn_chunk_uw_c{C}", lambda C=C: gdn_chunk_workload(8, 4096, 32, C, 10, 2)))
+        jobs.append(("lpbq_expand_4096x14336", lambda: lpbq_expand_workload(4096, 14336, 20, 3)))
         for key, job in jobs:
             if args.only and not re.search(args.only, key):
                 continue
