@@ -5,13 +5,14 @@
 //   1. the 16x16 diagonal blocks T_II = (I - A_II)^-1 for I >= J, by forward substitution with
 //      one lane per column (16 lanes per block, 16 blocks per round across the 4 waves);
 //   2. X_J = T_JJ, then for I = J+1 .. C/16-1 (block forward substitution)
-//         G   = sum_{K=J}^{I-1} A_IK X_K      (MFMA, the K range split across the 4 waves)
-//         X_I = T_II G                         (MFMA)
+//         G   = sum_{K=J}^{I-1} A_IK X_K      (MFMA; wave w takes the blocks K - J = w, w+4, ...)
+//         X_I = T_II G                         (MFMA, by the wave that owns block I - J)
 //      -- the block merge T_ij = T_ii * sum_{k=j}^{i-1} A_ik T_kj of the reference core
 //      (example/gdn_native/solve_op/src/gdn_solve_core.h:55-75), evaluated column-panel-wise.
-// The next two row blocks of A are prefetched into registers while the current block is
-// multiplied, and the barriers wait for LDS traffic only, so the chain of dependent block steps
-// is not paced by global-memory latency.
+// The chain of dependent block steps is the critical path, so a step has one barrier: the A
+// operands come straight from global memory into registers (two row blocks ahead), each wave
+// keeps the X blocks it owns in LDS in the MFMA lane layout (written and read by that wave
+// only), and only the partial sums of G cross waves (double-buffered by step parity).
 // Precision: QH_GDN_FP32 uses v_mfma_f32_16x16x4_f32; QH_GDN_BF16 feeds the G products through
 // v_mfma_f32_16x16x32_bf16 (fp32 accumulation) and keeps the diagonal solves and T_II G in fp32.
 // The u16 variant applies the GdnSolve op's code contract on load / store
@@ -74,48 +75,47 @@ __device__ __forceinline__ float4 load_a4(const GdnArgs &g, size_t idx) {
 
 template <bool U16, bool BF16>
 __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
-  // LDS: diagonal inverses of blocks J..nb-1, the solved panel rows, one staged A row block
-  // (16 rows x up to 240 columns), and per-wave partial products.
-  __shared__ float tdiag[kMaxNb][16][17];
-  __shared__ float xs[kMaxNb * 16][16];
+  // LDS: diagonal inverses of blocks J..nb-1 (rows padded to 20 floats so a lane reads 4
+  // adjacent columns with one 16-byte load), one staged A row block for the diagonal solves,
+  // the solved panel blocks in the MFMA lane layout, and double-buffered per-wave partial sums.
+  __shared__ __attribute__((aligned(16))) float tdiag[kMaxNb][16][20];
   __shared__ float abuf[16][kMaxNb * 16 + 4];
-  __shared__ float gpart[4][16][17];
+  __shared__ float4 xs[kMaxNb][64];
+  __shared__ float4 gpart[2][4][64];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int J = blockIdx.x, head = blockIdx.y;
   const int C = g.C, nb = g.nb;
   const size_t hbase = static_cast<size_t>(head) * C * C;
   const int c0 = J * 16;
+  // MFMA lane roles: r = row of the A operand / column of B and of the result, kq = k quarter.
+  // The k index of product step s is 4 kq + s, so a lane's result rows 4 kq .. 4 kq + 3 (one
+  // float4) are exactly its B operand for the next product.
+  const int r = lane & 15, kq = lane >> 4;
+  // Panel blocks are handed to the waves in units of UB blocks (one 16x16x4 f32 MFMA per k step,
+  // or two blocks per 16x16x32 bf16 MFMA): wave w owns units w, w + 4, ...
+  constexpr int UB = BF16 ? 2 : 1;
 
   // ---- zero the panel above its diagonal block ------------------------------------------
   for (int e = t; e < c0 * 16; e += kGdnThreads) {
-    const int r = e >> 4, c = e & 15;
-    store_t<U16>(g, hbase + static_cast<size_t>(r) * C + c0 + c, 0.0f);
+    const int rr = e >> 4, c = e & 15;
+    store_t<U16>(g, hbase + static_cast<size_t>(rr) * C + c0 + c, 0.0f);
   }
 
-  float4 pre0[4], pre1[4];
-  auto prefetch = [&](int I, float4 (&pre)[4]) {
-    const int L = 16 * (I - J), q = L / 4;
+  // A values of row block I that this wave multiplies: for each of its units i (kb0 = UB (wave
+  // + 4 i)), row 16 I + r, columns 16 (J + kb) + 4 kq .. + 3 of the unit's UB blocks.
+  float4 pre0[4][UB], pre1[4][UB];
+  auto prefetch = [&](int I, float4 (&pre)[4][UB]) {
+    const int n = I - J;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = t + u * kGdnThreads;
-      if (e < 16 * q) {
-        const int r = e / q, c4 = e % q;
-        pre[u] = load_a4<U16>(g, hbase + static_cast<size_t>(I * 16 + r) * C + c0 + 4 * c4);
-      }
-    }
-  };
-  auto commit = [&](int I, const float4 (&pre)[4]) {
-    const int L = 16 * (I - J), q = L / 4;
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = t + u * kGdnThreads;
-      if (e < 16 * q) {
-        const int r = e / q, c4 = e % q;
-        abuf[r][4 * c4 + 0] = pre[u].x;
-        abuf[r][4 * c4 + 1] = pre[u].y;
-        abuf[r][4 * c4 + 2] = pre[u].z;
-        abuf[r][4 * c4 + 3] = pre[u].w;
+      for (int h = 0; h < UB; ++h) {
+        const int kb = UB * (wave + 4 * i) + h;
+        if (kb < n)
+          pre[i][h] = load_a4<U16>(g, hbase + static_cast<size_t>(I * 16 + r) * C + (J + kb) * 16 + 4 * kq);
+        else
+          pre[i][h] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
   };
@@ -138,10 +138,10 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
       float x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float s = (i == j) ? 1.0f : 0.0f;
+        float sacc = (i == j) ? 1.0f : 0.0f;
 #pragma unroll
-        for (int k = 0; k < i; ++k) s = fmaf(abuf[i][b * 16 + k], x[k], s);
-        x[i] = s;
+        for (int k = 0; k < i; ++k) sacc = fmaf(abuf[i][b * 16 + k], x[k], sacc);
+        x[i] = sacc;
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) tdiag[I - J][i][j] = x[i];
@@ -152,67 +152,65 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
   // ---- X_J = T_JJ ----------------------------------------------------------------------------
   {
     const int i = t >> 4, j = t & 15;
-    const float v = tdiag[0][i][j];
-    xs[i][j] = v;
-    store_t<U16>(g, hbase + static_cast<size_t>(c0 + i) * C + c0 + j, v);
+    store_t<U16>(g, hbase + static_cast<size_t>(c0 + i) * C + c0 + j, tdiag[0][i][j]);
+    if (wave == 0)  // the owner of block 0 keeps it in the lane layout
+      xs[0][lane] = make_float4(tdiag[0][4 * kq][r], tdiag[0][4 * kq + 1][r], tdiag[0][4 * kq + 2][r],
+                                tdiag[0][4 * kq + 3][r]);
   }
 
   // ---- block forward substitution down the panel -------------------------------------------
-  // Row block I needs A[16I .. 16I+15][c0 .. 16I-1]: 16 rows x L columns, L = 16 (I - J).
-  // Each thread holds up to 4 float4 of a block (16 * 240 / 4 / 256 < 4); two blocks are in
-  // flight ahead of the one being multiplied.
-  // Row blocks alternate between the two prefetch slots (a register copy between slots would
-  // wait for the load in flight).
-  auto step = [&](const int I, float4 (&pre)[4]) __attribute__((always_inline)) {
-    lds_barrier();  // xs rows of the previous block visible; abuf free
-    commit(I, pre);
-    lds_barrier();
-    if (I + 2 < nb) prefetch(I + 2, pre);  // the slot just committed takes block I + 2
-    const int L = 16 * (I - J);
-    // partial G over this wave's 16-wide K blocks
+  //   G_I = sum_{K=J}^{I-1} A_IK X_K   (each wave over its own blocks, A from registers, X_K from
+  //                                     the wave's own LDS blocks)
+  //   X_I = T_II G_I                   (only the wave that owns block I - J, after one barrier)
+  // Each block X_K is written and later read by the same wave, so one barrier per row block
+  // (for the partial sums) is the only synchronisation of the chain.
+  auto step = [&](const int I, float4 (&pre)[4][UB]) __attribute__((always_inline)) {
+    const int n = I - J;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    const int r = lane & 15, kq = lane >> 4;
-    if (!BF16) {
-      for (int kb = wave; kb < I - J; kb += 4) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int k = kb * 16 + 4 * s + kq;
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(abuf[r][k], xs[k][r], acc, 0, 0, 0);
-        }
-      }
-    } else {
-      // 32-deep bf16 steps: wave w takes steps w, w+4, ...; the last half step is zero-padded.
-      const int steps = (L + 31) / 32;
-      for (int st = wave; st < steps; st += 4) {
-        v8bf a, b;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int k = st * 32 + 8 * kq + jj;
-          const bool ok = k < L;
-          a[jj] = static_cast<__bf16>(ok ? abuf[r][k] : 0.0f);
-          b[jj] = static_cast<__bf16>(ok ? xs[k][r] : 0.0f);
-        }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      const int kb0 = UB * (wave + 4 * i);
+      if (kb0 >= n) break;
+      if (!BF16) {
+        const float4 a = pre[i][0], x = xs[kb0][lane];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, x.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, x.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, x.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, x.w, acc, 0, 0, 0);
+      } else {
+        // k = 8 kq + jj: jj < 4 from block kb0, jj >= 4 from block kb0 + 1 (zero past the panel)
+        const float4 x0 = xs[kb0][lane];
+        const float4 x1 = kb0 + 1 < n ? xs[kb0 + 1][lane] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 a0 = pre[i][0], a1 = pre[i][UB - 1];
+        v8bf av, bv;
+        av[0] = static_cast<__bf16>(a0.x); av[1] = static_cast<__bf16>(a0.y);
+        av[2] = static_cast<__bf16>(a0.z); av[3] = static_cast<__bf16>(a0.w);
+        av[4] = static_cast<__bf16>(a1.x); av[5] = static_cast<__bf16>(a1.y);
+        av[6] = static_cast<__bf16>(a1.z); av[7] = static_cast<__bf16>(a1.w);
+        bv[0] = static_cast<__bf16>(x0.x); bv[1] = static_cast<__bf16>(x0.y);
+        bv[2] = static_cast<__bf16>(x0.z); bv[3] = static_cast<__bf16>(x0.w);
+        bv[4] = static_cast<__bf16>(x1.x); bv[5] = static_cast<__bf16>(x1.y);
+        bv[6] = static_cast<__bf16>(x1.z); bv[7] = static_cast<__bf16>(x1.w);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
       }
     }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) gpart[wave][4 * kq + q][r] = acc[q];
+    if (I + 2 < nb) prefetch(I + 2, pre);  // this slot's registers take row block I + 2
+    gpart[I & 1][wave][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
     lds_barrier();
-    if (wave == 0) {
-      // G (summed over waves) as the B operand of X_I = T_II G
+    if (wave == (n / UB) % 4) {
+      // G_I rows 4 kq .. 4 kq + 3 of column r, summed over the waves, as the B operand
+      const float4 p0 = gpart[I & 1][0][lane], p1 = gpart[I & 1][1][lane], p2 = gpart[I & 1][2][lane],
+                   p3 = gpart[I & 1][3][lane];
+      const float4 tr = *reinterpret_cast<const float4 *>(&tdiag[n][r][4 * kq]);
       v4f x = {0.f, 0.f, 0.f, 0.f};
+      x = __builtin_amdgcn_mfma_f32_16x16x4f32(tr.x, (p0.x + p1.x) + (p2.x + p3.x), x, 0, 0, 0);
+      x = __builtin_amdgcn_mfma_f32_16x16x4f32(tr.y, (p0.y + p1.y) + (p2.y + p3.y), x, 0, 0, 0);
+      x = __builtin_amdgcn_mfma_f32_16x16x4f32(tr.z, (p0.z + p1.z) + (p2.z + p3.z), x, 0, 0, 0);
+      x = __builtin_amdgcn_mfma_f32_16x16x4f32(tr.w, (p0.w + p1.w) + (p2.w + p3.w), x, 0, 0, 0);
+      xs[n][lane] = make_float4(x[0], x[1], x[2], x[3]);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int k = 4 * s + kq;
-        const float gk = gpart[0][k][r] + gpart[1][k][r] + gpart[2][k][r] + gpart[3][k][r];
-        x = __builtin_amdgcn_mfma_f32_16x16x4f32(tdiag[I - J][r][k], gk, x, 0, 0, 0);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = 4 * kq + q;
-        xs[L + row][r] = x[q];
-        store_t<U16>(g, hbase + static_cast<size_t>(I * 16 + row) * C + c0 + r, x[q]);
-      }
+      for (int q = 0; q < 4; ++q)
+        store_t<U16>(g, hbase + static_cast<size_t>(I * 16 + 4 * kq + q) * C + c0 + r, x[q]);
     }
   };
   for (int I = J + 1; I < nb; I += 2) {

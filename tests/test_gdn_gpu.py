@@ -38,6 +38,7 @@ def test_gdn_solve_config4_inputs(gpu, C, precision):
     Tref = og.inverse_fp64(A.astype(np.float64))
     err = og.oc(T, Tref)
     tol = FP32_TOL if precision == 0 else BF16_TOL
+    print(f"[gdn] C={C} precision={precision} oc={err:.3e}", flush=True)
     assert err <= tol, f"oc={err:.3e} > {tol:.1e}"
     # exact structure: zeros above the diagonal, unit diagonal
     iu = np.triu_indices(C, 1)
@@ -53,6 +54,7 @@ def test_gdn_solve_full_config4(gpu):
     for precision, tol in ((0, FP32_TOL), (1, BF16_TOL)):
         print(f"[gdn] config4 32x256 precision={precision}", flush=True)
         err = og.oc(solve(A, gpu, precision), Tref)
+        print(f"[gdn] config4 32x256 precision={precision} oc={err:.3e}", flush=True)
         assert err <= tol, f"precision {precision}: oc={err:.3e}"
 
 
