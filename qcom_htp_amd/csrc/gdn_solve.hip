@@ -12,7 +12,8 @@
 // The chain of dependent block steps is the critical path, so a step has one barrier: the A
 // operands come straight from global memory into registers (two row blocks ahead), each wave
 // keeps the X blocks it owns in LDS in the MFMA lane layout (written and read by that wave
-// only), and only the partial sums of G cross waves (double-buffered by step parity).
+// only), only the partial sums of G cross waves (double-buffered by step parity), and T is
+// written out after the chain.
 // Precision: QH_GDN_FP32 uses v_mfma_f32_16x16x4_f32; QH_GDN_BF16 feeds the G products through
 // v_mfma_f32_16x16x32_bf16 (fp32 accumulation) and keeps the diagonal solves and T_II G in fp32.
 // The u16 variant applies the GdnSolve op's code contract on load / store
@@ -40,12 +41,6 @@ struct GdnArgs {
   int zpA, zpT;
   float sA, sT, inv_sT;
 };
-
-template <bool U16>
-__device__ __forceinline__ float load_a(const GdnArgs &g, size_t idx) {
-  if (U16) return static_cast<float>(static_cast<int>(static_cast<const uint16_t *>(g.A)[idx]) - g.zpA) * g.sA;
-  return static_cast<const float *>(g.A)[idx];
-}
 
 template <bool U16>
 __device__ __forceinline__ void store_t(const GdnArgs &g, size_t idx, float v) {
@@ -96,12 +91,6 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
   // or two blocks per 16x16x32 bf16 MFMA): wave w owns units w, w + 4, ...
   constexpr int UB = BF16 ? 2 : 1;
 
-  // ---- zero the panel above its diagonal block ------------------------------------------
-  for (int e = t; e < c0 * 16; e += kGdnThreads) {
-    const int rr = e >> 4, c = e & 15;
-    store_t<U16>(g, hbase + static_cast<size_t>(rr) * C + c0 + c, 0.0f);
-  }
-
   // A values of row block I that this wave multiplies: for each of its units i (kb0 = UB (wave
   // + 4 i)), row 16 I + r, columns 16 (J + kb) + 4 kq .. + 3 of the unit's UB blocks.
   float4 pre0[4][UB], pre1[4][UB];
@@ -121,11 +110,27 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
   };
   // ---- diagonal inverses T_II, I = J .. nb-1 ----------------------------------------------
   for (int base = J; base < nb; base += 16) {
-    // stage the 16x16 diagonal blocks of this round
-    for (int e = t; e < 16 * 256; e += kGdnThreads) {
-      const int b = e >> 8, i = (e >> 4) & 15, k = e & 15;
+    // stage the 16x16 diagonal blocks of this round: every load is issued before the first LDS
+    // write (a load-then-store loop would wait for each load in turn)
+    float4 dv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = t + u * kGdnThreads;  // float4 slot: block e / 64, row (e / 4) % 16, quarter e % 4
+      const int b = e >> 6, i = (e >> 2) & 15, k4 = e & 3;
       const int I = base + b;
-      if (I < nb) abuf[i][b * 16 + k] = load_a<U16>(g, hbase + static_cast<size_t>(I * 16 + i) * C + I * 16 + k);
+      if (I < nb) dv[u] = load_a4<U16>(g, hbase + static_cast<size_t>(I * 16 + i) * C + I * 16 + 4 * k4);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = t + u * kGdnThreads;
+      const int b = e >> 6, i = (e >> 2) & 15, k4 = e & 3;
+      if (base + b < nb) {
+        float *dst = &abuf[i][b * 16 + 4 * k4];
+        dst[0] = dv[u].x;
+        dst[1] = dv[u].y;
+        dst[2] = dv[u].z;
+        dst[3] = dv[u].w;
+      }
     }
     if (base == J) {  // the first two row blocks of the chain load under the diagonal solves
       if (J + 1 < nb) prefetch(J + 1, pre0);
@@ -149,14 +154,10 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
     lds_barrier();
   }
 
-  // ---- X_J = T_JJ ----------------------------------------------------------------------------
-  {
-    const int i = t >> 4, j = t & 15;
-    store_t<U16>(g, hbase + static_cast<size_t>(c0 + i) * C + c0 + j, tdiag[0][i][j]);
-    if (wave == 0)  // the owner of block 0 keeps it in the lane layout
-      xs[0][lane] = make_float4(tdiag[0][4 * kq][r], tdiag[0][4 * kq + 1][r], tdiag[0][4 * kq + 2][r],
-                                tdiag[0][4 * kq + 3][r]);
-  }
+  // ---- X_J = T_JJ (kept by wave 0, the owner of block 0, in the lane layout) -----------------
+  if (wave == 0)
+    xs[0][lane] = make_float4(tdiag[0][4 * kq][r], tdiag[0][4 * kq + 1][r], tdiag[0][4 * kq + 2][r],
+                              tdiag[0][4 * kq + 3][r]);
 
   // ---- block forward substitution down the panel -------------------------------------------
   //   G_I = sum_{K=J}^{I-1} A_IK X_K   (each wave over its own blocks, A from registers, X_K from
@@ -208,14 +209,28 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_panel_kernel(GdnArgs g) {
       x = __builtin_amdgcn_mfma_f32_16x16x4f32(tr.z, (p0.z + p1.z) + (p2.z + p3.z), x, 0, 0, 0);
       x = __builtin_amdgcn_mfma_f32_16x16x4f32(tr.w, (p0.w + p1.w) + (p2.w + p3.w), x, 0, 0, 0);
       xs[n][lane] = make_float4(x[0], x[1], x[2], x[3]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        store_t<U16>(g, hbase + static_cast<size_t>(I * 16 + 4 * kq + q) * C + c0 + r, x[q]);
     }
   };
   for (int I = J + 1; I < nb; I += 2) {
     step(I, pre0);
     if (I + 1 < nb) step(I + 1, pre1);
+  }
+
+  // ---- write the panel: every global store comes after the chain ---------------------------
+  // (stores count in the same in-order counter as the loads, so a store issued inside the chain
+  // would make the wait for the next row block's A operands wait for it too)
+  for (int kb = 0; kb < nb - J; ++kb) {
+    if ((kb / UB) % 4 != wave) continue;  // each wave writes the blocks it owns
+    const float4 x = xs[kb][lane];
+    const size_t row0 = static_cast<size_t>((J + kb) * 16 + 4 * kq) * C + c0 + r;
+    store_t<U16>(g, hbase + row0, x.x);
+    store_t<U16>(g, hbase + row0 + C, x.y);
+    store_t<U16>(g, hbase + row0 + 2 * static_cast<size_t>(C), x.z);
+    store_t<U16>(g, hbase + row0 + 3 * static_cast<size_t>(C), x.w);
+  }
+  for (int e = t; e < c0 * 16; e += kGdnThreads) {  // zeros above the diagonal block
+    const int rr = e >> 4, c = e & 15;
+    store_t<U16>(g, hbase + static_cast<size_t>(rr) * C + c0 + c, 0.0f);
   }
 }
 
