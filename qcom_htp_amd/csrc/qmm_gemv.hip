@@ -53,6 +53,18 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 }
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// int8 weight bytes of 4 int4 codes: nibbles u (offset-binary, code = u - 8) times the LPBQ block
+// scale f, as (u * f + 128 - 8 f) ^ 0x80 per byte.  u * f <= 240 and 128 - 8 f >= 0 keep every
+// byte of the product and the sum below 256 (no carries between bytes); f = 0 gives zero weights.
+__device__ __forceinline__ uint32_t w4_to_i8(uint32_t u4, uint32_t f) {
+  return (u4 * f + (128u - 8u * f) * 0x01010101u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
+  return static_cast<long>((static_cast<unsigned long>(hi) << 32) | lo);
+}
 
 // Workgroup barrier for data exchanged through LDS: waits for this wave's LDS operations
 // only.  __syncthreads() would also wait for every global load in flight (its release fence),
@@ -339,15 +351,62 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   // Workgroups loop over groups only for 16 rows (whose staging is amortised over several
   // groups); otherwise each workgroup owns exactly one group.
   constexpr bool kLoop = MM == 16;
+  // 16 rows: the k-group products run on the matrix core (the dot4 path reads every activation
+  // row from LDS once per weight word and is LDS bound there)
+  constexpr bool kMfma = MM == 16;
   for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
-    int acc[MM], acc2[A16 ? MM : 1];
+    int acc[kMfma ? 1 : MM], acc2[A16 && !kMfma ? MM : 1];
 #pragma unroll
-    for (int m = 0; m < MM; ++m) {
+    for (int m = 0; m < (kMfma ? 1 : MM); ++m) {
       acc[m] = 0;
-      if (A16) acc2[m] = 0;
+      if (A16 && !kMfma) acc2[m] = 0;
     }
+    v4i macc = {0, 0, 0, 0}, macc2 = {0, 0, 0, 0};
     for (int i0 = 0; i0 < iters; i0 += kU) {
       if (i0 > 0) issue(grp, i0);
+      if constexpr (kMfma) {
+        // 16 rows: v_mfma_i32_16x16x32_i8 over the k-groups of the wave's 4 lane quarters.  In
+        // product j, lane quarter sub contributes k = 32 kg + 8 j .. + 7 of its own k-group kg to
+        // the B operand (its column) and to the A operand (activation row lane & 15), so the
+        // four products j cover each lane quarter's 32 k.
+        const int mrow = min(lane & 15, M - 1);  // rows past M repeat row M - 1 (never stored)
+#pragma unroll
+        for (int i = 0; i < kU; ++i) {
+          const int kg_raw = 4 * (wave + 4 * (i0 + i)) + sub;
+          const bool valid = kg_raw < KG;
+          const int kg = valid ? kg_raw : KG - 1;
+          uint32_t b[8];  // B operand dwords of products j = 0..3 (two each)
+          if (FMT == kTileI4) {
+            const uint32_t f = valid ? (LPBQ ? ((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu : 1u) : 0u;
+            const uint4 v = wv[i][0];
+            // byte j of the 16: k = j (low nibble), k = j + 16 (high nibble)
+            b[0] = w4_to_i8(v.x & 0x0F0F0F0Fu, f); b[1] = w4_to_i8(v.y & 0x0F0F0F0Fu, f);
+            b[2] = w4_to_i8(v.z & 0x0F0F0F0Fu, f); b[3] = w4_to_i8(v.w & 0x0F0F0F0Fu, f);
+            b[4] = w4_to_i8((v.x >> 4) & 0x0F0F0F0Fu, f); b[5] = w4_to_i8((v.y >> 4) & 0x0F0F0F0Fu, f);
+            b[6] = w4_to_i8((v.z >> 4) & 0x0F0F0F0Fu, f); b[7] = w4_to_i8((v.w >> 4) & 0x0F0F0F0Fu, f);
+          } else {
+            const uint4 v0 = wv[i][0], v1 = wv[i][FMT == kTileI4 ? 0 : 1];
+            const uint32_t mk = valid ? 0xFFFFFFFFu : 0u;
+            b[0] = v0.x & mk; b[1] = v0.y & mk; b[2] = v0.z & mk; b[3] = v0.w & mk;
+            b[4] = v1.x & mk; b[5] = v1.y & mk; b[6] = v1.z & mk; b[7] = v1.w & mk;
+          }
+          const uint2 *ap = reinterpret_cast<const uint2 *>(lds + static_cast<size_t>(mrow) * K + kg * 32);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint2 a = ap[j];
+            macc = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(b[2 * j], b[2 * j + 1]), macc, 0, 0, 0);
+          }
+          if (A16) {
+            const uint2 *lp = reinterpret_cast<const uint2 *>(lds + static_cast<size_t>(M + mrow) * K + kg * 32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint2 a = lp[j];
+              macc2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(b[2 * j], b[2 * j + 1]), macc2, 0, 0, 0);
+            }
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < kU; ++i) {
         const int kg_raw = 4 * (wave + 4 * (i0 + i)) + sub;
@@ -392,8 +451,16 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     // the next group's first batch is in flight during the reduction and the epilogue
     if (kLoop && grp + static_cast<int>(gridDim.x) < groups) issue(grp + gridDim.x, 0);
     // reduce over the 4 k-group lanes of each column, then over the waves in LDS
+    if constexpr (kMfma) {
+      // the product already summed the wave's lanes: lane (quarter q, column c) holds rows 4 q .. + 3
 #pragma unroll
-    for (int m = 0; m < MM; ++m) {
+      for (int q = 0; q < 4; ++q) {
+        red[wave][4 * sub + q][col] = macc[q];
+        if (A16) red2[wave][4 * sub + q][col] = macc2[q];
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < (kMfma ? 0 : MM); ++m) {
       acc[m] += __shfl_xor(acc[m], 16, 64);
       acc[m] += __shfl_xor(acc[m], 32, 64);
       if (sub == 0) red[wave][m][col] = acc[m];
