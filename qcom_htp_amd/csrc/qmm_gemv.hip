@@ -342,9 +342,17 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   if (t == 0) fix_cnt = 0;
   lds_barrier();
   if (t < units) store_unit<A16, FMT>(g, t, au, lds, r1);
-  for (int u = t + kGemvThreads; u < units; u += kGemvThreads) {
-    load_unit<A16>(g, u, au);
-    store_unit<A16, FMT>(g, u, au, lds, r1);
+  // further units: for 16 rows a batch of loads is issued before its first LDS store (a
+  // load-then-store loop would wait for every load in turn); fewer rows have one or two units
+  // per thread and no registers to spare under their occupancy bound
+  constexpr int kStageB = MM < 16 ? 1 : (A16 ? 4 : 8);
+  for (int u0 = t + kGemvThreads; u0 < units; u0 += kGemvThreads * kStageB) {
+    ActUnit<A16> ub[kStageB];
+#pragma unroll
+    for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(u0 + j * kGemvThreads, units - 1), ub[j]);
+#pragma unroll
+    for (int j = 0; j < kStageB; ++j)
+      if (u0 + j * kGemvThreads < units) store_unit<A16, FMT>(g, u0 + j * kGemvThreads, ub[j], lds, r1);
   }
   lds_barrier();
 
