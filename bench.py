@@ -20,6 +20,21 @@ import sys
 import time
 from pathlib import Path
 
+
+def _cpu_threads() -> int:
+    """Host threads for the CPU baseline: the job's CPU share (OMP_NUM_THREADS when the
+    environment sets it, else the CPUs this process may run on)."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+# BLAS / OpenMP thread counts are read when numpy is first imported: pin them before that.
+CPU_THREADS = _cpu_threads()
+for _var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+    os.environ[_var] = str(CPU_THREADS)
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -52,9 +67,20 @@ def time_kernel(fn, steps: int, warmup: int):
     return wall, ev
 
 
-def gemm_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, check_rows: int = 0,
-                  lpbq_block: int = 64):
+def parity_check(case, got) -> dict:
+    """Every output of the timed launches against the oracle (after the timed region)."""
     import numpy as np
+
+    from oracle import qmm as oq  # the checker, never the thing measured
+
+    want = oq.expected_output_case(case)
+    bad = int((got.astype(np.int64) != want.astype(np.int64)).sum())
+    if bad:
+        raise RuntimeError(f"{case.family.name} {case.m}x{case.k}x{case.n}: {bad} outputs differ from the oracle")
+    return {"parity_outputs_checked": int(got.size), "parity_mismatches": bad}
+
+
+def gemm_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, lpbq_block: int = 64):
     import torch
 
     from qcom_htp_amd import cases
@@ -68,14 +94,7 @@ def gemm_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     wall, ev = time_kernel(lambda i: op(act, out=out, path=PATH_GEMM), steps, warmup)
     ops = 2.0 * m * k * n
     res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "tops": ops / (ev * 1e-3) / 1e12}
-    if check_rows:
-        from oracle import qmm as oq  # parity spot check only
-
-        sub = cases.QmmCase(**{**case.__dict__, "activation_q": case.activation_q[:check_rows], "m": check_rows})
-        want = oq.expected_output_case(sub)
-        got = out[:check_rows].cpu().numpy()
-        res["parity_rows_checked"] = check_rows
-        res["parity_mismatches"] = int((got.astype(np.int64) != want.astype(np.int64)).sum())
+    res.update(parity_check(case, out.cpu().numpy()))
     op.close()
     return res, case
 
@@ -105,6 +124,7 @@ def gemv_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     wall /= steps
     if not torch.equal(out, want):
         raise RuntimeError(f"{family} GEMV: graph replay differs from the eager launch")
+    check = parity_check(case, out.cpu().numpy())
     info = ops[0].info
     act_b = m * k * (2 if family.endswith("a16") or "a16" in family else 1)
     out_b = m * n * (2 if "a16" in family else 1)
@@ -112,7 +132,7 @@ def gemv_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     nbytes = info["gemv_weight_bytes"] + per_ch + act_b + out_b
     res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "bytes": nbytes,
            "gbs": nbytes / (ev * 1e-3) / 1e9, "weight_copies": copies,
-           "rotated_mb": copies * info["gemv_weight_bytes"] / 1e6}
+           "rotated_mb": copies * info["gemv_weight_bytes"] / 1e6, **check}
     for o in ops:
         o.close()
     return res
@@ -136,8 +156,14 @@ def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
     out = torch.empty_like(a)
     wall, ev = time_kernel(lambda i: gdn_solve(a, precision=precision, out=out), steps, warmup)
     flops = (2.0 / 3.0) * C ** 3 * heads
+    from oracle import gdn as og  # the checker
+
+    err = og.oc(out.cpu().numpy(), og.inverse_fp64(A))
+    tol = og.GATE_FP32 if precision == 0 else og.GATE_BF16
+    if not err <= tol:
+        raise RuntimeError(f"GDN solve C={C} precision={precision}: oc {err:.3e} > {tol:.1e}")
     return {"heads": heads, "C": C, "precision": "fp32" if precision == 0 else "bf16", "ms": ev, "wall_ms": wall,
-            "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12}, A
+            "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12, "oc_vs_fp64": err}, A
 
 
 def gdn_chunk_workload(B: int, T: int, H: int, C: int, steps: int, warmup: int):
@@ -159,48 +185,103 @@ def gdn_chunk_workload(B: int, T: int, H: int, C: int, steps: int, warmup: int):
     # dense algorithmic work per chunk-head: A = K K^T (2 C^2 D), inverse (2/3 C^3), W and U (2 C^2 D each)
     flops = chunk_heads * (3 * 2.0 * C * C * D + (2.0 / 3.0) * C ** 3)
     nbytes = B * T * H * (4 * D * 2 + 2 * 4)  # K, V in + W, U out (bf16) + beta, g (fp32)
+    # after the timed region: the outputs of a sample of (batch, chunk, head) items, first and
+    # last included, against the float64 solve
+    import numpy as np
+
+    from oracle import gdn as og  # the checker
+
+    w, u = gdn_chunk_uw(k, v, gc, beta, C)
+    nch = T // C
+    worst = 0.0
+    for it in np.linspace(0, chunk_heads - 1, 8).astype(int).tolist():
+        h, c, b = it % H, (it // H) % nch, it // (H * nch)
+        sl = slice(c * C, (c + 1) * C)
+        kc, vc = (x[b, sl, h].double().cpu().numpy() for x in (k, v))
+        bc, gcc = beta[b, sl, h].double().cpu().numpy(), gc[b, sl, h].double().cpu().numpy()
+        U, W = og.chunk_uw(og.inverse_fp64(og.build_A(kc, bc, gcc)), kc, vc, bc, gcc)
+        worst = max(worst, og.oc(u[b, sl, h].double().cpu().numpy(), U), og.oc(w[b, sl, h].double().cpu().numpy(), W))
+    if not worst <= og.GATE_BF16:
+        raise RuntimeError(f"GDN chunk C={C}: oc {worst:.3e} > {og.GATE_BF16}")
     return {"B": B, "T": T, "H": H, "C": C, "ms": ev, "wall_ms": wall, "chunk_heads_per_s": chunk_heads / (ev * 1e-3),
-            "tflops_alg": flops / (ev * 1e-3) / 1e12, "bytes": nbytes, "gbs": nbytes / (ev * 1e-3) / 1e9}
+            "tflops_alg": flops / (ev * 1e-3) / 1e12, "bytes": nbytes, "gbs": nbytes / (ev * 1e-3) / 1e9,
+            "oc_vs_fp64_worst_of_8_items": worst}
 
 
 def cpu_baseline(case, gdn_A):
-    """The oracle (numpy/LAPACK restatement of the reference's CPU path) on host cores."""
+    """The oracle (numpy/LAPACK/torch restatement of the reference's CPU path) on the host cores
+    of this job: one warm-up, then the median of 5 runs per shape (3 for the slowest)."""
     import numpy as np
+    import torch
 
     from oracle import gdn as og
     from oracle import qmm as oq
     from qcom_htp_amd import cases
 
+    torch.set_num_threads(CPU_THREADS)
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"), default=1)
+        blas = max((p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"), default=1)
     except Exception:  # pragma: no cover
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+        blas = CPU_THREADS
+
+    def med(fn, reps=5):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    def rows_of(c, r):
+        return cases.QmmCase(**{**c.__dict__, "activation_q": c.activation_q[:r], "m": r})
+
+    shapes = {}
+    # primary: W4A8 per-channel at 4096^3, sampled to 1024 of the 4096 rows
     rows = 1024
-    sub = cases.QmmCase(**{**case.__dict__, "activation_q": case.activation_q[:rows], "m": rows})
-    oq.expected_output_case(cases.QmmCase(**{**case.__dict__, "activation_q": case.activation_q[:64], "m": 64}))
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        oq.expected_output_case(sub)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    ops = 2.0 * rows * case.k * case.n
-    g_heads = 8
-    t0 = time.perf_counter()
-    og.inverse_fp64(gdn_A[:g_heads])
-    tg = time.perf_counter() - t0
+    sub = rows_of(case, rows)
+    t = med(lambda: oq.expected_output_case(sub))
+    value = 2.0 * rows * case.k * case.n / t / 1e12
+    # 256^3, the seven seeded u8i8 cases
+    c1 = [cases.make_case("u8i8", cn, 256, 256, 256) for cn in cases.CASES]
+    t = med(lambda: [oq.expected_output_case(c) for c in c1])
+    shapes["u8i8_256^3_7_cases"] = {"s": t, "tops": 7 * 2.0 * 256 ** 3 / t / 1e12}
+    # LPBQ at K=4096, N=14336: 512 prefill rows, and the decode shapes M=16 and M=1
+    for fam in ("w4a8_lpbq", "w4a16_lpbq"):
+        c = cases.synthetic_case(fam, 512, 4096, 14336, seed=2, lpbq_block=64)
+        for m in (512, 16, 1):
+            sc = rows_of(c, m)
+            t = med(lambda: oq.expected_output_case(sc), reps=5 if m == 512 else 3)
+            shapes[f"{fam}_{m}x4096x14336"] = {"s": t, "tops": 2.0 * m * 4096 * 14336 / t / 1e12}
+    # GDN solve at C=256 x 32 heads: LAPACK inverse per head, and the reference's float64 row
+    # recurrence in torch
+    t = med(lambda: og.inverse_fp64(gdn_A))
+    shapes["gdn_inverse_c256_h32_lapack"] = {"s": t, "heads_per_s": gdn_A.shape[0] / t}
+    At = torch.from_numpy(np.ascontiguousarray(gdn_A))
+    t = med(lambda: og.forward_subst_torch(At), reps=3)
+    shapes["gdn_forward_subst_c256_h32_torch"] = {"s": t, "heads_per_s": gdn_A.shape[0] / t}
+    # the intra-chunk half of the chunked GDN (A-build, row recurrence, U and W) in torch
+    # float64, on a sample of chunk-heads
+    rng = np.random.default_rng(8)
+    for C, n in ((64, 256), (256, 32)):
+        kk = torch.from_numpy(rng.standard_normal((n, C, 128)))
+        vv = torch.from_numpy(rng.standard_normal((n, C, 128)))
+        bb = torch.sigmoid(torch.from_numpy(rng.standard_normal((n, C))))
+        gg = torch.nn.functional.logsigmoid(torch.from_numpy(rng.standard_normal((n, C))) + 3.0)
+        t = med(lambda: og.chunk_stage_a_torch(kk, vv, gg, bb), reps=3)
+        shapes[f"gdn_chunk_uw_c{C}_torch"] = {"s": t, "chunk_heads": n, "chunk_heads_per_s": n / t}
     return {
-        "value": ops / t / 1e12,
+        "value": value,
         "unit": "TOPS",
-        "cores": int(threads),
+        "cores": int(CPU_THREADS),
         "kind": "port",
         "sample": f"oracle output_ref_q (float64 dgemm + requant) on {rows} of {case.m} rows of the "
-                  f"{case.k}x{case.n} W4A8 case, median of 3",
-        "gdn_heads_per_s": g_heads / tg,
-        "gdn_sample": f"np.linalg.inv(I - A) float64 on {g_heads} heads of C={gdn_A.shape[-1]}",
+                  f"{case.k}x{case.n} W4A8 case; one warm-up, median of 5",
+        "blas_threads": int(blas),
         "affinity_cpus": len(os.sched_getaffinity(0)),
+        "shapes": shapes,
     }
 
 
@@ -274,7 +355,7 @@ def main() -> int:
 
     M = K = N = 4096
     log("primary: w4a8_per_channel GEMM 4096^3")
-    prim, case = gemm_workload("w4a8_per_channel", M, K, N, args.steps, args.warmup, check_rows=64)
+    prim, case = gemm_workload("w4a8_per_channel", M, K, N, args.steps, args.warmup)
     extra = {"w4a8_gemm_4096": prim}
     gdn_A = None
     if not args.quick:
@@ -325,7 +406,7 @@ def main() -> int:
         "extra": extra,
     }
     if not args.quick and not args.only:
-        log("cpu baseline (oracle on host cores)")
+        log(f"cpu baseline (oracle on {CPU_THREADS} host threads)")
         line["cpu_baseline"] = cpu_baseline(case, gdn_A)
     print(json.dumps(line), flush=True)
     return 0

@@ -219,6 +219,16 @@ qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const fl
                           void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
                           uint32_t head_dim, uint32_t chunk, uint32_t flags, void *stream);
 
+/* qh_gdn_chunk_uw with a cap on the persistent grid: at most max_workgroups workgroups walk the
+ * (batch, chunk, head) items (0 = as many as are resident on the device at once).  A cap leaves
+ * compute units to concurrent work on other streams; results do not depend on it.  No
+ * counterpart in the reference (its chunk loop is the sequential Python of
+ * scripts/gdn_ref_kernel.py:91-101). */
+qh_status qh_gdn_chunk_uw_ex(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
+                             void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
+                             uint32_t head_dim, uint32_t chunk, uint32_t flags, uint32_t max_workgroups,
+                             void *stream);
+
 #ifdef __cplusplus
 }
 #endif

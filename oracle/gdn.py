@@ -19,6 +19,10 @@ Functions and the reference lines they follow
                          example/gdn_native/solve_op/gdn_solve_ref.c:19-69.
 * ``chunk_uw``        -- U = T (beta * V), W = T (beta * K) [or T (beta * K * e^g)],
                          scripts/gdn_ref_kernel.py:88-89.
+* ``forward_subst_torch`` / ``chunk_stage_a_torch`` -- the same row recurrence and the whole
+                         intra-chunk stage (l2norm, A-build, recurrence, U, W) in torch float64,
+                         batched over heads as the reference runs them
+                         (scripts/gdn_ref_kernel.py:71-89); the CPU baseline times these.
 
 Pinning
 -------
@@ -29,6 +33,8 @@ Pinning
   /root/reference (oracle/_ref/gdn_solve_ref, built by oracle/Makefile) on the same codes.
 * ``build_A`` is pinned by closed-form special cases (beta = 0 -> A = 0; orthogonal keys ->
   A = 0; a rank-one check on two tokens).
+* ``forward_subst_torch`` and ``chunk_stage_a_torch`` are pinned against LAPACK's inverse
+  (``inverse_fp64``) with ``build_A`` / ``chunk_uw``.
 """
 
 from __future__ import annotations
@@ -46,6 +52,8 @@ __all__ = [
     "dequantize_u16",
     "solve_int16_blocks",
     "chunk_uw",
+    "forward_subst_torch",
+    "chunk_stage_a_torch",
     "GATE_BF16",
     "GATE_FP32",
     "SA_REF",
@@ -160,3 +168,42 @@ def chunk_uw(T: np.ndarray, k: np.ndarray, v: np.ndarray, beta: np.ndarray, gc: 
     if decay_w:
         kb = kb * np.exp(np.cumsum(gc.astype(np.float64), axis=-1))[..., None]
     return U, T @ kb
+
+
+def forward_subst_torch(A):
+    """(I - A)^-1 of strictly-lower A [..., C, C] by the reference's row recurrence, in torch
+    float64 (scripts/gdn_ref_kernel.py:84-87)."""
+    import torch
+
+    A = torch.as_tensor(A, dtype=torch.float64)
+    C = A.shape[-1]
+    T = torch.tril(A, -1).clone()
+    for i in range(1, C):
+        row = T[..., i, :i].clone()
+        T[..., i, :i] = row + torch.einsum("...j,...jk->...k", row, T[..., :i, :i])
+    return T + torch.eye(C, dtype=torch.float64)
+
+
+def chunk_stage_a_torch(k, v, gc, beta, decay_w: bool = True):
+    """The intra-chunk stage of the reference GDN kernel on [n, C, D] keys / values and [n, C]
+    per-token log decays / betas, torch float64 (scripts/gdn_ref_kernel.py:71-89): l2norm,
+    k_beta / v_beta, g = cumsum, A = -(k_beta k^T) decay below the diagonal, the row recurrence,
+    U = T v_beta, W = T (k_beta [e^g]).  Returns (U, W)."""
+    import torch
+
+    k = torch.as_tensor(k, dtype=torch.float64)
+    v = torch.as_tensor(v, dtype=torch.float64)
+    gc = torch.as_tensor(gc, dtype=torch.float64)
+    beta = torch.as_tensor(beta, dtype=torch.float64)
+    C = k.shape[-2]
+    kn = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    v_beta = v * beta.unsqueeze(-1)
+    k_beta = kn * beta.unsqueeze(-1)
+    g = torch.cumsum(gc, dim=-1)
+    lower = torch.tril(torch.ones(C, C, dtype=torch.bool), -1)
+    decay = torch.exp(torch.where(lower, g.unsqueeze(-1) - g.unsqueeze(-2), torch.zeros((), dtype=torch.float64)))
+    A = -(k_beta @ kn.transpose(-1, -2)) * decay * lower
+    T = forward_subst_torch(A)
+    U = T @ v_beta
+    W = T @ (k_beta * torch.exp(g).unsqueeze(-1) if decay_w else k_beta)
+    return U, W

@@ -62,6 +62,7 @@ EXPORTED = (
     "qh_gdn_solve_f32",
     "qh_gdn_solve_u16",
     "qh_gdn_chunk_uw",
+    "qh_gdn_chunk_uw_ex",
 )
 
 
@@ -144,6 +145,8 @@ def _declare(L: C.CDLL) -> None:
     L.qh_gdn_solve_u16.restype = st
     L.qh_gdn_chunk_uw.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp]
     L.qh_gdn_chunk_uw.restype = st
+    L.qh_gdn_chunk_uw_ex.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, vp]
+    L.qh_gdn_chunk_uw_ex.restype = st
 
 
 def lib() -> C.CDLL:

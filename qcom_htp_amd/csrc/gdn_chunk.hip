@@ -495,7 +495,7 @@ __global__ __launch_bounds__(chunk_threads<NB>(), 1) void gdn_chunk_kernel(const
 }
 
 template <int NB, bool OUT_F32>
-qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
+qh_status launch_nb(const ChunkArgs &a, int max_wg, hipStream_t stream) {
   const long long items = static_cast<long long>(a.B) * a.nchunks * a.H;  // (batch, chunk, head)
   if (items > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: too many chunks");
   if (items == 0) return QH_STATUS_OK;
@@ -515,6 +515,7 @@ qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
     grid_slots = (per_cu < 1 ? 1 : per_cu) * cus;
     if (dev >= 0 && dev < kMaxDevices) slots[dev].store(grid_slots, std::memory_order_relaxed);
   }
+  if (max_wg > 0 && max_wg < grid_slots) grid_slots = max_wg;  // caller's cap on the persistent grid
   const long long grid = grid_slots < items ? grid_slots : items;
   hipLaunchKernelGGL((gdn_chunk_kernel<NB, OUT_F32>), dim3(static_cast<unsigned>(grid)), dim3(chunk_threads<NB>()), 0,
                      stream, a, static_cast<int>(items));
@@ -524,14 +525,14 @@ qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
 }
 
 template <int NB>
-qh_status launch_nb(const ChunkArgs &a, hipStream_t stream) {
-  return a.out_f32 ? launch_nb<NB, true>(a, stream) : launch_nb<NB, false>(a, stream);
+qh_status launch_nb(const ChunkArgs &a, int max_wg, hipStream_t stream) {
+  return a.out_f32 ? launch_nb<NB, true>(a, max_wg, stream) : launch_nb<NB, false>(a, max_wg, stream);
 }
 
 }  // namespace
 
 qh_status launch_gdn_chunk_uw(const uint16_t *k, const uint16_t *v, const float *g, const float *beta, void *w,
-                              void *u, int B, int T, int H, int C, int flags, hipStream_t stream) {
+                              void *u, int B, int T, int H, int C, int flags, int max_wg, hipStream_t stream) {
   ChunkArgs a{};
   a.k = k;
   a.v = v;
@@ -548,11 +549,11 @@ qh_status launch_gdn_chunk_uw(const uint16_t *k, const uint16_t *v, const float 
   a.out_f32 = (flags & QH_GDN_OUT_F32) != 0;
   switch (C) {
     case 64:
-      return launch_nb<4>(a, stream);
+      return launch_nb<4>(a, max_wg, stream);
     case 128:
-      return launch_nb<8>(a, stream);
+      return launch_nb<8>(a, max_wg, stream);
     case 256:
-      return launch_nb<16>(a, stream);
+      return launch_nb<16>(a, max_wg, stream);
     default:
       return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: chunk %d (need 64, 128 or 256)", C);
   }

@@ -159,9 +159,10 @@ qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t head
 }
 
 
-qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
-                          void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
-                          uint32_t head_dim, uint32_t chunk, uint32_t flags, void *stream) {
+qh_status qh_gdn_chunk_uw_ex(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
+                             void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
+                             uint32_t head_dim, uint32_t chunk, uint32_t flags, uint32_t max_workgroups,
+                             void *stream) {
   if (!k_dev || !v_dev || !g_dev || !beta_dev || !w_dev || !u_dev)
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_uw: NULL buffer");
   if (head_dim != 128) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_uw: head_dim=%u (need 128)", head_dim);
@@ -177,9 +178,20 @@ qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const fl
   const uintptr_t al = reinterpret_cast<uintptr_t>(k_dev) | reinterpret_cast<uintptr_t>(v_dev) |
                        reinterpret_cast<uintptr_t>(w_dev) | reinterpret_cast<uintptr_t>(u_dev);
   if (al % 16) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_uw: k, v, w, u must be 16-byte aligned");
+  if (max_workgroups > (1u << 24))
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_uw: max_workgroups=%u (0 = device-resident grid)",
+                max_workgroups);
   return launch_gdn_chunk_uw(k_dev, v_dev, g_dev, beta_dev, w_dev, u_dev, static_cast<int>(batch),
                              static_cast<int>(tokens), static_cast<int>(heads), static_cast<int>(chunk),
-                             static_cast<int>(flags), static_cast<hipStream_t>(stream));
+                             static_cast<int>(flags), static_cast<int>(max_workgroups),
+                             static_cast<hipStream_t>(stream));
+}
+
+qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
+                          void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
+                          uint32_t head_dim, uint32_t chunk, uint32_t flags, void *stream) {
+  return qh_gdn_chunk_uw_ex(k_dev, v_dev, g_dev, beta_dev, w_dev, u_dev, batch, tokens, heads, head_dim, chunk, flags,
+                            0, stream);
 }
 
 }  // extern "C"

@@ -1,5 +1,6 @@
-// Decode-shape (M <= 16) quantized GEMV: HBM streaming of packed weights with dwordx4 loads,
-// int8 dot4 MACs (v_dot4_i32_i8) and wavefront reductions -- no MFMA.
+// Decode-shape (M <= 16) quantized GEMV: HBM streaming of packed weights with dwordx4 loads and
+// wavefront reductions; the k-group products are int8 dot4 MACs (v_dot4_i32_i8) for up to 4
+// rows and i8 matrix-core products (v_mfma_i32_16x16x32_i8) for 5..16 rows.
 //
 // Weight stream layout (prepared once): [N/16 column groups][K/32 k-groups][16 columns][bytes],
 // 16 B per (column, k-group) for int4 (byte j: low nibble k=j, high nibble k=j+16,
@@ -15,11 +16,17 @@
 //
 // Arithmetic: activations are staged once per workgroup in LDS as signed int8 planes
 // (a - 128 for 8-bit; hi / lo' bytes of a - 32768 for 16-bit) together with their sums over
-// each 32-k group.  Int4 codes are used as the unsigned nibble u = code + 8 (a mask, no sign
-// extension): sum_k a'_k (u_k - 8) f = f (dot4(a', u) - 8 sum_k a'_k) per k-group, exact in
-// int32 (f = the LPBQ block scale, 1 otherwise).  The four waves' partial sums meet in LDS;
-// each output is then requantised by one thread with the GEMM's rounding rules (t in float64,
-// exact fixup of outputs within the certified margin of a rounding boundary).
+// each 32-k group.  Two paths compute the k-group products, both exact in int32:
+//   * up to 4 rows (dot4): int4 codes are used as the unsigned nibble u = code + 8 (a mask, no
+//     sign extension): sum_k a'_k (u_k - 8) f = f (dot4(a', u) - 8 sum_k a'_k) per k-group
+//     (f = the LPBQ block scale, 1 otherwise);
+//   * 5..16 rows (matrix core): the weight words of a lane are the B operand of
+//     v_mfma_i32_16x16x32_i8 and the staged rows the A operand; int4 codes are widened to int8
+//     in registers with the block scale folded in, (u f + 128 - 8 f) ^ 0x80 per byte, which needs
+//     u f <= 240 and 8 f <= 128, i.e. f <= 16 (the range prepare accepts).
+// The four waves' partial sums meet in LDS; each output is then requantised by one thread
+// with the GEMM's rounding rules (t in float64, exact fixup of outputs within the certified
+// margin of a rounding boundary).
 
 #include <atomic>
 
@@ -551,10 +558,13 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   }
 }
 
-// Raises the kernel's dynamic LDS limit once per device (the call costs a driver round trip,
-// too much for a launch that streams 30 MB in a few microseconds).
-template <class Kernel>
-qh_status allow_dyn_lds(Kernel kernel) {
+// Raises the dynamic LDS limit of one kernel instantiation once per device (the call costs a
+// driver round trip, too much for a launch that streams 30 MB in a few microseconds).  The
+// cache is keyed by the instantiation's template arguments: every instantiation has the same
+// function type, so a cache keyed by that type would be shared by all of them.
+template <bool A16, int FMT, bool LPBQ, int MM>
+qh_status allow_dyn_lds() {
+  const auto kernel = &qmm_gemv_kernel<A16, FMT, LPBQ, MM>;
   static std::atomic<uint32_t> done{0};  // bit d: set on device d
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -570,7 +580,7 @@ qh_status allow_dyn_lds(Kernel kernel) {
 
 template <bool A16, int FMT, bool LPBQ, int MM>
 qh_status launch_one(const GemvArgs &g, dim3 grid, size_t dyn_lds, hipStream_t stream) {
-  const qh_status st = allow_dyn_lds(&qmm_gemv_kernel<A16, FMT, LPBQ, MM>);
+  const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, MM>();
   if (st != QH_STATUS_OK) return st;
   hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MM>), grid, dim3(kGemvThreads), dyn_lds, stream, g);
   const hipError_t err = hipGetLastError();

@@ -126,5 +126,5 @@ qh_status launch_gdn_solve_u16(const uint16_t *A, uint16_t *T, int heads, int C,
 qh_status launch_lpbq_expand(const uint8_t *codes, const uint8_t *scales, uint8_t *out, uint32_t K, uint32_t N,
                              hipStream_t stream);
 qh_status launch_gdn_chunk_uw(const uint16_t *k, const uint16_t *v, const float *g, const float *beta, void *w,
-                              void *u, int B, int T, int H, int C, int flags, hipStream_t stream);
+                              void *u, int B, int T, int H, int C, int flags, int max_wg, hipStream_t stream);
 }  // namespace qh

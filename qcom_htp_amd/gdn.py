@@ -64,10 +64,11 @@ def GdnSolve(A_codes: torch.Tensor, zpA: int, sA: float, zpT: int, sT: float, pr
 
 def gdn_chunk_uw(k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor, chunk: int,
                  decay_w: bool = False, out_dtype: torch.dtype = torch.bfloat16,
-                 stream: Optional[torch.cuda.Stream] = None):
+                 stream: Optional[torch.cuda.Stream] = None, max_workgroups: int = 0):
     """(W, U) [B, T, H, 128] from k, v bf16 [B, T, H, 128] and g (per-token log decay), beta
     float32 [B, T, H]: U = T (beta v), W = T (beta l2norm(k)) [times e^g when decay_w], with
-    T = (I - A)^-1 of each chunk of ``chunk`` tokens."""
+    T = (I - A)^-1 of each chunk of ``chunk`` tokens.  ``max_workgroups`` caps the persistent
+    grid (0: every workgroup the device holds at once)."""
     for name, x, dt in (("k", k, torch.bfloat16), ("v", v, torch.bfloat16), ("g", g, torch.float32),
                         ("beta", beta, torch.float32)):
         if x.device.type != "cuda" or x.dtype != dt or not x.is_contiguous():
@@ -80,7 +81,7 @@ def gdn_chunk_uw(k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.
     w = torch.empty((B, T, H, D), dtype=out_dtype, device=k.device)
     u = torch.empty_like(w)
     flags = (W_DECAY if decay_w else 0) | (_lib.QH_GDN_OUT_F32 if out_dtype == torch.float32 else 0)
-    st = _lib.lib().qh_gdn_chunk_uw(k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), w.data_ptr(),
-                                    u.data_ptr(), B, T, H, D, chunk, flags, _stream(stream))
+    st = _lib.lib().qh_gdn_chunk_uw_ex(k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), w.data_ptr(),
+                                       u.data_ptr(), B, T, H, D, chunk, flags, int(max_workgroups), _stream(stream))
     _lib.check(st, "qh_gdn_chunk_uw")
     return w, u

@@ -113,3 +113,29 @@ def test_chunk_uw_solves_the_triangular_system():
         if decay_w:
             kb = kb * np.exp(np.cumsum(gc))[:, None]
         np.testing.assert_allclose(ImA @ W, kb, rtol=0, atol=1e-10)
+
+
+def test_torch_row_recurrence_matches_lapack():
+    import torch
+
+    k, beta, gc = og.config4_inputs(heads=3, C=96, seed=12)
+    A = og.build_A(k, beta, gc)
+    T = og.forward_subst_torch(torch.from_numpy(A)).numpy()
+    assert og.oc(T, og.inverse_fp64(A)) < 1e-12
+
+
+@pytest.mark.parametrize("decay_w", [False, True])
+def test_torch_stage_a_matches_lapack_products(decay_w):
+    import torch
+
+    rng = np.random.default_rng(13)
+    n, C = 3, 64
+    k = rng.standard_normal((n, C, 128))
+    v = rng.standard_normal((n, C, 128))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((n, C))))
+    gc = -np.logaddexp(0.0, -(rng.standard_normal((n, C)) + 3.0))
+    U, W = og.chunk_stage_a_torch(torch.from_numpy(k), torch.from_numpy(v), torch.from_numpy(gc),
+                                  torch.from_numpy(beta), decay_w=decay_w)
+    Uref, Wref = og.chunk_uw(og.inverse_fp64(og.build_A(k, beta, gc)), k, v, beta, gc, decay_w=decay_w)
+    assert og.oc(U.numpy(), Uref) < 1e-12
+    assert og.oc(W.numpy(), Wref) < 1e-12
