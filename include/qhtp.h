@@ -55,6 +55,13 @@ typedef enum qh_weight_format {
   QH_WEIGHT_I4 = 1,      /* int4 codes in [-7, 7] (one per int8), per-output-channel scale */
   QH_WEIGHT_I4_LPBQ = 2, /* int4 codes in [-7, 7] times a per-(channel, K-block) integer  */
                          /* scale in [1, 16], under a per-output-channel scale             */
+  QH_WEIGHT_I4_GROUP = 3, /* int4 codes in [-7, 7] (int8 storage, [-127, 127] accepted) with */
+                          /* one float32 scale per (channel, group_size-deep K group) and a  */
+                          /* float bias: the per-group schema of                             */
+                          /* generate_qnn_matmul_python_cases.py:392-423,460-470             */
+  QH_WEIGHT_I16 = 4,     /* int16 codes [N][K] (weight16_nk): the W16A16 weight, computed as */
+                         /* two int8 byte planes (docs/w16a16_is_two_w8a16.md:13-45); only   */
+                         /* qh_qmm_accumulate and qh_qmm_run_contract apply to it            */
 } qh_weight_format;
 
 /*
@@ -92,7 +99,13 @@ typedef struct qh_qmm_desc {
   const int8_t *weight_nk;         /* [N][K] int codes                                  */
   const uint8_t *lpbq_block_scale; /* [N][K / lpbq_block] in [1, 16] (LPBQ only)         */
   const float *weight_scale;       /* [N] per-output-channel scale, > 0                 */
-  const int32_t *bias_q;           /* [N] int32 bias codes at act_scale*weight_scale, or NULL */
+  const int32_t *bias_q;           /* [N] int32 bias codes at act_scale*weight_scale, or NULL; */
+                                   /* the integer contracts add it as it is              */
+  /* Per-group and int16 weights (fields after bias_q are read only for these formats). */
+  const float *group_scale;        /* [N][K / group_size] float32 scales (QH_WEIGHT_I4_GROUP) */
+  uint32_t group_size;             /* K depth of a scale group: 64, 128, 256, ... (I4_GROUP)  */
+  const float *bias_float;         /* [N] float bias added unquantised (I4_GROUP), or NULL   */
+  const int16_t *weight16_nk;      /* [N][K] int16 codes (QH_WEIGHT_I16)                     */
 } qh_qmm_desc;
 
 typedef struct qh_qmm_prepared qh_qmm_prepared;
@@ -103,7 +116,9 @@ qh_status qh_qmm_prepare(const qh_qmm_desc *desc, qh_qmm_prepared **out);
 
 /* out_dev[M][N] (uint8 or uint16, row-major) from act_dev[M][K] (uint8 or uint16,
  * row-major; the reference's [1, M/32, 32, K] activation is this layout).  Picks the
- * MFMA GEMM for M > 16 and the streaming GEMV for M <= 16. */
+ * MFMA GEMM for M > 16 and the streaming GEMV for M <= 16.  Per-group weights run on the
+ * exact integer GEMM for every M; QH_WEIGHT_I16 returns QH_STATUS_UNSUPPORTED (use
+ * qh_qmm_run_contract). */
 qh_status qh_qmm_run(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
                      void *stream);
 
@@ -112,9 +127,38 @@ qh_status qh_qmm_run_path(const qh_qmm_prepared *prep, uint32_t m, const void *a
                           uint32_t path, void *stream);
 
 /* Exact int32/int64 accumulators acc[M][N] = sum_k (act - act_zp) * w_int, written as
- * int64 (the integer-accumulator contract of scripts/reconstruct_hmx_u8_drain.py:10-16). */
+ * int64 (the integer-accumulator contract of scripts/reconstruct_hmx_u8_drain.py:10-16).
+ * w_int as for qh_qmm_run_contract (for QH_WEIGHT_I16: the int16 code, the identity
+ * acc = 256 (act - zp) @ hi + (act - zp) @ lo of scripts/verify_w16a16_two_w8a16.py:21-57). */
 qh_status qh_qmm_accumulate(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, int64_t *acc_dev,
                             void *stream);
+
+/* The reference's integer output contracts, applied to the exact integer dot product
+ * acc = sum_k (act - act_zp) * w_int of a prepared weight (w_int: the int8 / int4 code, code *
+ * block scale for LPBQ, the raw code for per-group, the int16 code for QH_WEIGHT_I16);
+ * qmax = 2^out_bits - 1, out_zp of the prepared descriptor, d = the divisor argument. */
+typedef enum qh_contract {
+  QH_CONTRACT_CLIP_I32 = 0,          /* clip(int32(acc + bias_q), 0, qmax), int32 arithmetic     */
+                                     /* wrapping like numpy's: the "legacy" contract of          */
+                                     /* gen_quant_chain.py:991-995 (_make_reference_step)        */
+  QH_CONTRACT_CLIP_I64 = 1,          /* clip(acc + bias_q, 0, qmax) in int64: the unit-scale LPBQ */
+                                     /* model hmx_w4a8_lpbq_scalar (HmxU8I4ToU8MatMulOp.cpp:210- */
+                                     /* 233) with act_zp = 0 and bias_q = its "effective" bias   */
+  QH_CONTRACT_DIV_RINT = 2,          /* clip(rint(double(acc) / d + out_zp), 0, qmax): the native */
+                                     /* A16 contract (gen_quant_chain.py:986-987, d = 127 for W8; */
+                                     /* d = 32767 is the W16A16 requantisation)                  */
+  QH_CONTRACT_FLOOR256_DIV_RINT = 3, /* as DIV_RINT on floor(acc / 256) * 256: the native W4A16  */
+                                     /* contract (gen_quant_chain.py:981-985, d = 7)             */
+  QH_CONTRACT_ROUND_DIV = 4,         /* clip(round_half_away(acc / d) + out_zp, 0, qmax):        */
+                                     /* hmx_w4a16_lpbq_scalar_native / round_div7               */
+                                     /* (HmxU16I4ToU16MatMulOp.cpp:520-568, d = 7)               */
+} qh_contract;
+
+/* out_dev[M][N] (uint8 / uint16 per out_bits) = contract(acc) for act_dev[M][K]; exact int64
+ * accumulation (i8 matrix cores), any M >= 1.  divisor >= 1 (ignored by the CLIP contracts).
+ * Replaces the reference's integer reference steps and scalar LPBQ fallbacks listed above. */
+qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
+                              uint32_t contract, uint32_t divisor, void *stream);
 
 typedef struct qh_qmm_info {
   uint32_t k, n, act_bits, out_bits, weight_format, lpbq_block;

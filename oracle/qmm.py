@@ -17,6 +17,11 @@ Functions and the reference lines they follow
   example/qnn_hmx_matmul_common/gen_quant_chain.py:971-996.
 * ``w4a8_lpbq_scalar`` -- HmxU8I4ToU8MatMulOp.cpp:210-233 on logical arrays.
 * ``w4a16_lpbq_scalar_native`` / ``round_div7`` -- HmxU16I4ToU16MatMulOp.cpp:514-568.
+* ``contract_output``  -- the integer output contracts above on an exact accumulator, one
+  function (legacy clip in int32 arithmetic, int64 clip, native ``rint(acc / qmax + zp)``
+  with and without the floor-256 step, round-half-away division).
+* ``split_int16`` / ``w16a16_accumulator`` -- the W16A16 = two W8A16 passes identity,
+  scripts/verify_w16a16_two_w8a16.py:21-57 (q16 = 256 hi + lo, hi signed, lo unsigned).
 
 Pinning
 -------
@@ -28,7 +33,12 @@ Pinning
 * ``reference_step``, ``w4a8_lpbq_scalar``, ``w4a16_lpbq_scalar_native``: pinned by
   closed-form special cases (zero activations at the zero point give the bias /
   the output zero point; single-k impulses give rank-1 products; round_div7 on
-  +-(7q+3), +-(7q+4) ties) in tests/test_oracle_qmm.py.
+  +-(7q+3), +-(7q+4) ties) in tests/test_oracle_qmm.py, and by exact-rational rounding
+  (``fractions.Fraction``) and Python-integer brute force on small random inputs.
+* ``contract_output``: pinned against ``reference_step`` / ``w4a8_lpbq_scalar`` /
+  ``w4a16_lpbq_scalar_native`` on the same accumulators, against exact-rational rounding
+  (odd divisors leave no ties) and against Python-integer loops with explicit int32 wrap.
+* ``w16a16_accumulator``: pinned by Python-integer brute force and the byte-split identity.
 """
 
 from __future__ import annotations
@@ -44,26 +54,44 @@ __all__ = [
     "w4a8_lpbq_scalar",
     "round_div7",
     "w4a16_lpbq_scalar_native",
+    "contract_output",
+    "round_div",
+    "split_int16",
+    "w16a16_accumulator",
+    "CONTRACT_NAMES",
 ]
 
 
 def _weight_deq(w_int_nk: np.ndarray, w_scale: np.ndarray) -> np.ndarray:
-    """fl32(w_int * s32): the float32 product the reference stores as ``w_deq``."""
-    return w_int_nk.astype(np.float32) * np.asarray(w_scale, dtype=np.float32)[:, None]
+    """fl32(w_int * s32): the float32 product the reference stores as ``w_deq``.  ``w_scale``
+    is per output channel [N], or per (channel, K-group) [N, G] for the per-group schema
+    (generate_qnn_matmul_python_cases.py:406-410)."""
+    s = np.asarray(w_scale, dtype=np.float32)
+    if s.ndim == 2:
+        k = w_int_nk.shape[1]
+        return w_int_nk.astype(np.float32) * np.repeat(s, k // s.shape[1], axis=1)
+    return w_int_nk.astype(np.float32) * s[:, None]
 
 
-def dequantized_output(x_q, w_int_nk, w_scale, bias_q, act_scale, act_zp):
-    """float64 ``quant_real = x_deq @ w_deq.T + bias_deq`` (generate_qnn_matmul_python_cases.py:447-473)."""
-    bias_scale = act_scale * np.asarray(w_scale, dtype=np.float32).astype(np.float64)
-    bias_deq = np.asarray(bias_q).astype(np.float64) * bias_scale
+def dequantized_output(x_q, w_int_nk, w_scale, bias_q, act_scale, act_zp, bias_float=None):
+    """float64 ``quant_real = x_deq @ w_deq.T + bias_deq`` (generate_qnn_matmul_python_cases.py:447-473).
+    Per-channel scales: ``bias_deq = bias_q * fl64(sA * s32)``; per-group scales: ``bias_deq``
+    is the float bias (:460-470)."""
+    s = np.asarray(w_scale, dtype=np.float32)
+    if s.ndim == 2:
+        n = s.shape[0]
+        bias_deq = (np.zeros(n) if bias_float is None else np.asarray(bias_float, dtype=np.float32).astype(np.float64))
+    else:
+        bias_scale = act_scale * s.astype(np.float64)
+        bias_deq = np.asarray(bias_q).astype(np.float64) * bias_scale
     x_deq = (np.asarray(x_q).astype(np.float64) + (-act_zp)) * act_scale
     w_deq = _weight_deq(np.asarray(w_int_nk), w_scale)
     return x_deq @ w_deq.astype(np.float64).T + bias_deq
 
 
-def expected_output(x_q, w_int_nk, w_scale, bias_q, act_scale, out_scale, act_zp, out_zp, out_bits):
+def expected_output(x_q, w_int_nk, w_scale, bias_q, act_scale, out_scale, act_zp, out_zp, out_bits, bias_float=None):
     """``output_ref_q`` of the reference (generate_qnn_matmul_python_cases.py:474-481)."""
-    qr = dequantized_output(x_q, w_int_nk, w_scale, bias_q, act_scale, act_zp)
+    qr = dequantized_output(x_q, w_int_nk, w_scale, bias_q, act_scale, act_zp, bias_float)
     qmax = (1 << out_bits) - 1
     q = np.rint(qr / out_scale - (-out_zp))
     dtype = np.dtype("<u2") if out_bits == 16 else np.dtype("uint8")
@@ -89,6 +117,7 @@ def expected_output_case(case):
         fam.act_zp,
         fam.out_zp,
         fam.out_bits,
+        getattr(case, "bias_float", None),
     )
 
 
@@ -155,3 +184,60 @@ def w4a16_lpbq_scalar_native(act_u16, w_kn) -> np.ndarray:
     """clip(round_div7(sum_k (a - 32768) * w) + 32768, 0, 65535) (:545-568)."""
     acc = (act_u16.astype(np.int64) - 32768) @ w_kn.astype(np.int64)
     return np.clip(round_div7(acc) + 32768, 0, 65535).astype(np.uint16)
+
+
+CONTRACT_NAMES = ("clip_i32", "clip_i64", "div_rint", "floor256_div_rint", "round_div")
+
+
+def round_div(v, d: int):
+    """Integer division rounding half away from zero: (|v| + d // 2) // d with v's sign (the
+    round_div7 rule of HmxU16I4ToU16MatMulOp.cpp:520-524 for any divisor d)."""
+    v = np.asarray(v, dtype=np.int64)
+    h = d // 2
+    return np.where(v >= 0, (v + h) // d, -((-v + h) // d))
+
+
+def contract_output(acc, contract: str, divisor: int = 1, bias_q=None, out_zp: int = 0, out_bits: int = 8):
+    """One of the reference's integer output contracts on an exact accumulator acc [M, N]
+    (sum_k (a - zp) w_int):
+
+    * clip_i32          -- clip((acc + bias) in int32 arithmetic, 0, qmax): numpy's int32 matmul
+                           and add wrap modulo 2^32 (gen_quant_chain.py:991-995, legacy);
+    * clip_i64          -- clip(acc + bias, 0, qmax) in int64 (hmx_w4a8_lpbq_scalar,
+                           HmxU8I4ToU8MatMulOp.cpp:210-233, bias = its "effective" bias);
+    * div_rint          -- clip(rint(float64(acc) / d + out_zp)) (gen_quant_chain.py:986-987);
+    * floor256_div_rint -- the same after acc = floor(acc / 256) * 256 (:981-985);
+    * round_div         -- clip(round_half_away(acc / d) + out_zp) (HmxU16I4ToU16MatMulOp.cpp:545-568).
+    """
+    acc = np.asarray(acc, dtype=np.int64)
+    qmax = (1 << out_bits) - 1
+    dtype = np.dtype("<u2") if out_bits == 16 else np.dtype("uint8")
+    b = np.zeros(acc.shape[-1], np.int64) if bias_q is None else np.asarray(bias_q, dtype=np.int64)
+    if contract == "clip_i32":
+        v = (acc + b[None, :]).astype(np.int32)  # modulo 2^32, as numpy's int32 arithmetic
+        return np.clip(v, 0, qmax).astype(dtype)
+    if contract == "clip_i64":
+        return np.clip(acc + b[None, :], 0, qmax).astype(dtype)
+    if contract in ("div_rint", "floor256_div_rint"):
+        if contract == "floor256_div_rint":
+            acc = np.floor_divide(acc, 256) * 256
+        y = acc.astype(np.float64) / float(divisor)
+        return np.clip(np.rint(y + float(out_zp)), 0, qmax).astype(dtype)
+    if contract == "round_div":
+        return np.clip(round_div(acc, divisor) + out_zp, 0, qmax).astype(dtype)
+    raise ValueError(f"unknown contract {contract!r}")
+
+
+def split_int16(q16):
+    """q16 = 256 hi + lo with hi = q16 >> 8 (int8) and lo = q16 & 0xff (uint8)
+    (scripts/verify_w16a16_two_w8a16.py:21-28)."""
+    q = np.asarray(q16, dtype=np.int64)
+    return q >> 8, q & 0xFF
+
+
+def w16a16_accumulator(x_q, w16_nk, act_zp) -> np.ndarray:
+    """Exact int64 sum_k (x - zp) q16 as the two 8-bit-weight passes, combined with x 256:
+    (x - zp) @ hi * 256 + (x - zp) @ lo (scripts/verify_w16a16_two_w8a16.py:44-47)."""
+    hi, lo = split_int16(w16_nk)
+    a = np.asarray(x_q, dtype=np.int64) - act_zp
+    return (a @ hi.T) * 256 + a @ lo.T

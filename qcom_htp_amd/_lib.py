@@ -21,6 +21,15 @@ QH_STATUS_SHAPE_UNSUPPORTED = 4
 QH_WEIGHT_I8 = 0
 QH_WEIGHT_I4 = 1
 QH_WEIGHT_I4_LPBQ = 2
+QH_WEIGHT_I4_GROUP = 3
+QH_WEIGHT_I16 = 4
+
+# Integer output contracts (qh_contract).
+QH_CONTRACT_CLIP_I32 = 0
+QH_CONTRACT_CLIP_I64 = 1
+QH_CONTRACT_DIV_RINT = 2
+QH_CONTRACT_FLOOR256_DIV_RINT = 3
+QH_CONTRACT_ROUND_DIV = 4
 
 # Packed weight carriers (qh_weight_carrier) and their flags.
 CARRIERS = {
@@ -55,6 +64,7 @@ EXPORTED = (
     "qh_qmm_run",
     "qh_qmm_run_path",
     "qh_qmm_accumulate",
+    "qh_qmm_run_contract",
     "qh_qmm_query",
     "qh_qmm_release",
     "qh_weight_unpack",
@@ -90,6 +100,10 @@ class QmmDesc(C.Structure):
         ("lpbq_block_scale", C.c_void_p),
         ("weight_scale", C.c_void_p),
         ("bias_q", C.c_void_p),
+        ("group_scale", C.c_void_p),
+        ("group_size", C.c_uint32),
+        ("bias_float", C.c_void_p),
+        ("weight16_nk", C.c_void_p),
     ]
 
 
@@ -131,6 +145,8 @@ def _declare(L: C.CDLL) -> None:
     L.qh_qmm_run_path.restype = st
     L.qh_qmm_accumulate.argtypes = [vp, u32, vp, vp, vp]
     L.qh_qmm_accumulate.restype = st
+    L.qh_qmm_run_contract.argtypes = [vp, u32, vp, vp, u32, u32, vp]
+    L.qh_qmm_run_contract.restype = st
     L.qh_qmm_query.argtypes = [vp, C.POINTER(QmmInfo)]
     L.qh_qmm_query.restype = st
     L.qh_qmm_release.argtypes = [vp]

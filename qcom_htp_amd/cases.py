@@ -115,9 +115,11 @@ FAMILIES = {
     "w4a16_lpbq": _fam("w4a16_lpbq", 16, 4, 16, "lpbq_blockwise_expansion", "w4a16"),
 }
 
-# Families whose weight schema the GPU kernels implement (per-channel and LPBQ).
-# The per-group schema leaves its bias "not modelled" in the reference and is not
-# part of the gated set.
+# The families of the reference's promoted gates (per-channel and LPBQ).  The per-group
+# schema (K64 group scales, float bias: its bias contract is "not modelled" in the
+# reference, generate_qnn_matmul_python_cases.py:460-470) is implemented too but is not part
+# of that gated set.
+PER_GROUP_FAMILIES = ("w4a8_per_group", "w4a16_per_group")
 GATED_FAMILIES = (
     "u8i8",
     "w4a8_per_channel",
@@ -311,6 +313,7 @@ class QmmCase:
     lpbq_block_int_scale: Optional[np.ndarray] = None  # uint8 [N, K/block]
     lpbq_expanded_q_nk: Optional[np.ndarray] = None  # int16 [N,K]
     lpbq_pre_group_scale: Optional[np.ndarray] = None
+    bias_float: Optional[np.ndarray] = None  # float32 [N]: the per-group schema's float bias
     seed: Optional[int] = None
     extra: dict = field(default_factory=dict)
 
@@ -338,16 +341,20 @@ def make_case(family: Family | str, case: str, m: int, k: int, n: int) -> QmmCas
     float64 product ``x @ w.T + bias`` of the float sources, as in the reference.
     """
     fam = FAMILIES[family] if isinstance(family, str) else family
-    if fam.weight_schema == "per_group":
-        raise ValueError("per-group schema has no modelled bias contract; not supported")
     x, w, bias = make_float_case(fam, case, m, k, n)
     out_float = x.astype(np.float64) @ w.astype(np.float64).T + bias.astype(np.float64)
     act_scale = affine_scale_from_minmax(float(x.min()), float(x.max()), 0, fam.act_qmax, fam.act_zp)
     out_scale = affine_scale_from_minmax(float(out_float.min()), float(out_float.max()), 0, fam.out_qmax, fam.out_zp)
     x_q = quantize_affine(x, act_scale, -fam.act_zp, 0, fam.act_qmax, fam.act_dtype)
     wq = quantize_weight(fam, w)
-    bias_scale = act_scale * wq["scale"].astype(np.float64)
-    bias_q = np.clip(np.rint(bias.astype(np.float64) / bias_scale), -(1 << 31), (1 << 31) - 1).astype(np.int32)
+    bias_float = None
+    if wq["scale"].ndim == 1:
+        bias_scale = act_scale * wq["scale"].astype(np.float64)
+        bias_q = np.clip(np.rint(bias.astype(np.float64) / bias_scale), -(1 << 31), (1 << 31) - 1).astype(np.int32)
+    else:
+        # per-group scales: bias_q is all zeros and the float bias is added as it is (:460-470)
+        bias_q = np.zeros(n, np.int32)
+        bias_float = bias.astype(np.float32)
     return QmmCase(
         family=fam,
         case=case,
@@ -364,6 +371,7 @@ def make_case(family: Family | str, case: str, m: int, k: int, n: int) -> QmmCas
         lpbq_block_int_scale=wq.get("block_int_scale"),
         lpbq_expanded_q_nk=wq.get("expanded"),
         lpbq_pre_group_scale=wq.get("pre_group_scale"),
+        bias_float=bias_float,
         seed=seed_for(fam.name, case),
     )
 
@@ -385,7 +393,9 @@ def synthetic_case(
       per-tensor scale 0.02 (A8) / 1e-4 (A16) with the family's fixed zero point;
     * weights: symmetric int4 in [-7, 7] (int8 in [-127, 127] for W8); LPBQ weights are
       int4 with ``lpbq_block``-wide K blocks carrying integer scales in [1, lpbq_max_scale];
-    * per-output-channel float32 scales ~ U(1e-3, 1e-2); int32 bias ~ U(-2^15, 2^15).
+    * per-output-channel float32 scales ~ U(1e-3, 1e-2); int32 bias ~ U(-2^15, 2^15);
+    * per-group families: float32 scales ~ U(1e-3, 1e-2) per (channel, 64-k group) and a
+      float32 bias ~ U(-0.5, 0.5) (the per-group schema's bias is the float bias itself).
 
     The output scale, unless given, is fitted (as the reference fits it from the float
     output range) to the exact dequantised output of the first ``calib_rows`` rows.
@@ -404,7 +414,25 @@ def synthetic_case(
     bias_q = rng.integers(-(1 << 15), (1 << 15) + 1, size=n).astype(np.int32)
     block_scale = None
     expanded = None
+    bias_float = None
     w_int = q.astype(np.int16)
+    if fam.weight_schema == "per_group":
+        # per-(channel, 64-k group) float32 scales ~ U(1e-3, 1e-2); float bias ~ U(-0.5, 0.5)
+        gsz = fam.weight_group_size
+        if k % gsz:
+            raise ValueError(f"K={k} must be a multiple of the group size {gsz}")
+        s32 = rng.uniform(1.0e-3, 1.0e-2, size=(n, k // gsz)).astype(np.float32)
+        bias_q = np.zeros(n, np.int32)
+        bias_float = rng.uniform(-0.5, 0.5, size=n).astype(np.float32)
+        deq = q.astype(np.float32) * np.repeat(s32, gsz, axis=1)
+        if out_scale is None:
+            rows = min(calib_rows, m)
+            xd = (x_q[:rows].astype(np.float64) - fam.act_zp) * act_scale
+            qr = xd @ deq.astype(np.float64).T + bias_float.astype(np.float64)
+            out_scale = affine_scale_from_minmax(float(qr.min()), float(qr.max()), 0, fam.out_qmax, fam.out_zp)
+        return QmmCase(family=fam, case="synthetic", m=m, k=k, n=n, activation_q=x_q, weight_q_nk=q,
+                       weight_scale=s32, bias_q=bias_q, act_scale=float(act_scale), out_scale=float(out_scale),
+                       weight_deq=deq, bias_float=bias_float, seed=seed)
     if fam.is_lpbq:
         if k % lpbq_block:
             raise ValueError(f"K={k} must be a multiple of the LPBQ block {lpbq_block}")

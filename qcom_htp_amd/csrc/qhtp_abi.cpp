@@ -66,6 +66,12 @@ qh_status qh_qmm_run_path(const qh_qmm_prepared *prep, uint32_t m, const void *a
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: activation rows must be 16-byte aligned");
   if (path > 2) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run: unknown path %u", path);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (prep->shape.exact_only) {
+    if (prep->shape.wfmt == QH_WEIGHT_I16)
+      return fail(QH_STATUS_UNSUPPORTED, "qh_qmm_run: int16 weights have no float requantisation; use qh_qmm_run_contract");
+    // per-group weights: the exact integer GEMM for every M (path ignored)
+    return launch_qmm_exact(prep, static_cast<int>(m), act_dev, out_dev, 0, 0, 1, s);
+  }
   const bool gemv = path == 2 || (path == 0 && m <= 16 && gemv_fits(prep, static_cast<int>(m)));
   if (gemv) return launch_qmm_gemv(prep, static_cast<int>(m), act_dev, out_dev, s);
   return launch_qmm_gemm(prep, static_cast<int>(m), act_dev, out_dev, s);
@@ -83,7 +89,27 @@ qh_status qh_qmm_accumulate(const qh_qmm_prepared *prep, uint32_t m, const void 
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_accumulate: NULL buffer");
   if (reinterpret_cast<uintptr_t>(act_dev) % 16)
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_accumulate: activation must be 16-byte aligned");
+  if (prep->shape.exact_only)
+    return launch_qmm_exact(prep, static_cast<int>(m), act_dev, acc_dev, 1, 0, 1, static_cast<hipStream_t>(stream));
   return launch_qmm_accumulate(prep, static_cast<int>(m), act_dev, acc_dev, static_cast<hipStream_t>(stream));
+}
+
+qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
+                              uint32_t contract, uint32_t divisor, void *stream) {
+  if (prep == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: prepared handle is NULL");
+  if (m == 0 || m > (1u << 22)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_qmm_run_contract: bad M=%u", m);
+  if (act_dev == nullptr || out_dev == nullptr)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: NULL buffer");
+  if (reinterpret_cast<uintptr_t>(act_dev) % 16)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: activation must be 16-byte aligned");
+  if (contract > QH_CONTRACT_ROUND_DIV)
+    return fail(QH_STATUS_UNSUPPORTED, "qh_qmm_run_contract: unknown contract %u", contract);
+  const bool divides = contract == QH_CONTRACT_DIV_RINT || contract == QH_CONTRACT_FLOOR256_DIV_RINT ||
+                       contract == QH_CONTRACT_ROUND_DIV;
+  if (divides && (divisor == 0 || divisor > (1u << 30)))
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: divisor %u must be in [1, 2^30]", divisor);
+  return launch_qmm_exact(prep, static_cast<int>(m), act_dev, out_dev, 2, static_cast<int>(contract),
+                          divides ? static_cast<int>(divisor) : 1, static_cast<hipStream_t>(stream));
 }
 
 qh_status qh_qmm_query(const qh_qmm_prepared *prep, qh_qmm_info *info) {
@@ -110,7 +136,8 @@ qh_status qh_qmm_release(qh_qmm_prepared *prep) {
   QmmDevice &D = prep->dev;
   void *ptrs[] = {D.tiles, D.gemv_tiles, D.gemv_lpbq, D.alpha, D.beta, D.corr,
                   D.margin, D.absb, D.bias_deq, D.s32, D.mant, D.colsum, D.gemv_margin_r1,
-                  D.colsum_r, D.alpha_e, D.scale_exp, D.margin_exact, D.resid};
+                  D.colsum_r, D.alpha_e, D.scale_exp, D.margin_exact, D.resid, D.bias_q,
+                  D.corr_int, D.mult, D.corr_rq, D.s32g};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   (void)hipSetDevice(cur);

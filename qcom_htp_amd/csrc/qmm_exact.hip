@@ -1,0 +1,378 @@
+// Exact integer GEMM on gfx950 i8 MFMA (v_mfma_i32_32x32x32_i8): int64 sums
+//
+//     D[m][n] = sum_p sum_g  mult_p[g][n] * sum_{k in g} (a[m][k] - zp) * w_p[n][k]
+//             + ones * sum_k (a[m][k] - zp)                               (exact, int64)
+//
+// over one or two int8 weight planes w_p (stored in the GEMM tile layout) with integer
+// multipliers per (plane, 64-k group, channel), and an optional all-ones plane.  It serves the
+// weight schemas whose exact dot product is not a single int8 product times one per-channel
+// constant, and the reference's integer contracts:
+//   * per-group (K64) scales (generate_qnn_matmul_python_cases.py:392-423): with
+//     s_g = M_g 2^E_g (M_g a 24-bit integer) the oracle's float32 weight fl32(q s_g) is
+//     2^E_g (q M_g + r) for a small integer residue r, so with E_min = min_g E_g and
+//     d_g = E_g - E_min the dot product is exactly 2^E_min D for planes q (multiplier
+//     M_g 2^d_g) and r (multiplier 2^d_g);
+//   * int16 weights as two byte planes (docs/w16a16_is_two_w8a16.md:13-45): q16 = 256 hi +
+//     (lo - 128) + 128, planes hi (x 256) and lo - 128 (x 1) plus 128 x the all-ones plane;
+//   * the integer contracts (gen_quant_chain.py:963-996, HmxU8I4ToU8MatMulOp.cpp:210-233,
+//     HmxU16I4ToU16MatMulOp.cpp:514-568) on the exact accumulator of any prepared weight.
+// Activations enter the MFMA shifted to int8: a - 128 (8-bit), or 256 hi + lo' with
+// a - 32896 = 256 hi + lo' (16-bit; two MFMAs per product); the shift times the plane column
+// sums is a per-channel constant added at the end.  The int32 MFMA sums are moved into the
+// int64 accumulators every 64 k (|partial| < 2^30).
+//
+// Workgroup: 256 threads = 4 waves over a 64 x 64 output tile, one 32 x 32 block per wave;
+// fragments come straight from global memory (L2) into registers, one 32-k step ahead.
+// Requantisation (per-group): t = D alpha_e + beta in float64 is certain unless t lies within
+// the oracle's own float64 noise of a rounding boundary; those outputs are listed and
+// recomputed as the oracle forms its dot product (float64 products of fl64((a - zp) sA) and
+// fl32(q s_g)).
+
+#include <type_traits>
+#include <utility>
+
+#include "qmm_internal.h"
+
+namespace qh {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kExThreads = 256;
+constexpr int kExTile = 64;
+constexpr int kExFixCap = 512;
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Operand column of plane p, channel n in the tile layout (planes interleaved by 32 channels).
+__device__ __forceinline__ int plane_col(int p, int n, int lp) { return (n >> 5) * (32 * lp) + p * 32 + (n & 31); }
+
+__device__ __forceinline__ uint4 load_w16(const ExactArgs &g, int c, int k) {
+  const size_t tile = static_cast<size_t>(c / kBN) * g.KT + k / kBK;
+  return *reinterpret_cast<const uint4 *>(g.tiles + tile * (kBN * kBK) + tile_off_i8(c % kBN, k));
+}
+
+__device__ __forceinline__ void store_out(const ExactArgs &g, size_t idx, int v) {
+  if (g.out16)
+    static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(v);
+  else
+    static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(v);
+}
+
+// The reference's integer contracts on the exact accumulator D = sum_k (a - zp) w.
+__device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, int n) {
+  const long long qmax = g.out_qmax;
+  switch (g.contract) {
+    case QH_CONTRACT_CLIP_I32: {  // int32 arithmetic of the reference (wraps modulo 2^32)
+      const long long b = g.bias_q ? g.bias_q[n] : 0;
+      const int v = static_cast<int>(static_cast<unsigned int>(static_cast<unsigned long long>(D + b)));
+      return v < 0 ? 0 : (v > qmax ? static_cast<int>(qmax) : v);
+    }
+    case QH_CONTRACT_CLIP_I64: {
+      const long long v = D + (g.bias_q ? g.bias_q[n] : 0);
+      return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
+    }
+    case QH_CONTRACT_FLOOR256_DIV_RINT:
+      D = (D >> 8) * 256;  // floor division (arithmetic shift rounds toward -inf)
+      [[fallthrough]];
+    case QH_CONTRACT_DIV_RINT: {
+      const double y = static_cast<double>(D) / static_cast<double>(g.divisor);
+      const double o = rint(y + static_cast<double>(g.out_zp));
+      return static_cast<int>(fmin(fmax(o, 0.0), static_cast<double>(qmax)));
+    }
+    case QH_CONTRACT_ROUND_DIV: {
+      const long long d = g.divisor, h = d / 2;
+      const long long q = D >= 0 ? (D + h) / d : -((-D + h) / d);
+      const long long v = q + g.out_zp;
+      return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
+    }
+  }
+  return 0;
+}
+
+// The oracle's float64 dot product for output (m, n) of a per-group weight, by one wave:
+// sum_k fl64((a_k - zp) sA) * fl32(q_k s_g), then + bias, / sO, + zp, rint, clip.
+template <bool A16>
+__device__ void emulate_one(const ExactArgs &g, int m, int n, int lane) {
+  double s = 0.0;
+  const int c0 = plane_col(0, n, g.layout_planes);
+  for (int kc = lane; kc < g.K / 16; kc += 64) {
+    const int k = kc * 16;
+    const uint4 wv = load_w16(g, c0, k);
+    const float sc = g.s32g[static_cast<size_t>(n) * g.G + (k >> g.gshift)];
+    uint4 av[2];
+    if (A16) {
+      const uint4 *ap = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(g.act) + static_cast<size_t>(m) * g.K + k);
+      av[0] = ap[0];
+      av[1] = ap[1];
+    } else {
+      av[0] = *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(m) * g.K + k);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int a = A16 ? static_cast<int>(reinterpret_cast<const uint16_t *>(av)[j])
+                        : static_cast<int>(reinterpret_cast<const uint8_t *>(av)[j]);
+      const int w = reinterpret_cast<const int8_t *>(&wv)[j];
+      const float wd = static_cast<float>(w) * sc;
+      s = fma(static_cast<double>(a - g.act_zp) * g.sA, static_cast<double>(wd), s);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) {
+    const double t = (s + g.bias_deq[n]) / g.sO + static_cast<double>(g.out_zp);
+    const double o = fmin(fmax(rint(t), 0.0), static_cast<double>(g.out_qmax));
+    store_out(g, static_cast<size_t>(m) * g.N + n, static_cast<int>(o));
+  }
+}
+
+// Fragments of one 32-k step: activations (A16: two raw words) and the planes' weights.
+template <bool A16>
+struct Frag {
+  uint4 a[A16 ? 2 : 1];
+  uint4 b[2];
+};
+
+template <bool A16>
+__device__ __forceinline__ void load_step(const ExactArgs &g, int mrow, int ncol, int k, Frag<A16> &f) {
+  if (A16) {
+    const uint4 *ap = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(g.act) + static_cast<size_t>(mrow) * g.K + k);
+    f.a[0] = ap[0];
+    f.a[A16 ? 1 : 0] = ap[1];
+  } else {
+    f.a[0] = *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(mrow) * g.K + k);
+  }
+  f.b[0] = load_w16(g, plane_col(0, ncol, g.layout_planes), k);
+  f.b[1] = g.nplanes > 1 ? load_w16(g, plane_col(1, ncol, g.layout_planes), k) : make_uint4(0u, 0u, 0u, 0u);
+}
+
+template <bool A16, int MODE>
+__global__ __launch_bounds__(kExThreads) void qmm_exact_kernel(const ExactArgs g) {
+  constexpr int D = A16 ? 2 : 1;  // activation digits
+  __shared__ uint32_t fix_list[MODE == 0 ? kExFixCap : 1];
+  __shared__ int fix_cnt;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int m0 = blockIdx.y * kExTile + wm * 32, n0 = blockIdx.x * kExTile + wn * 32;
+  const int mrow = min(m0 + (lane & 31), g.M - 1);  // rows past M repeat the last row (never stored)
+  const int ncol = n0 + (lane & 31);                // < Np: padding columns hold zero weights
+  const int kq = 16 * (lane >> 5);                  // this lane's 16 k of a 32-k step
+  if (MODE == 0 && t == 0) fix_cnt = 0;
+
+  v16i acc[2][D], one[D];
+  long long acc64[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc64[j] = 0;
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    acc[0][d] = v16i{};
+    acc[1][d] = v16i{};
+    one[d] = v16i{};
+  }
+  const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  const int steps = g.K / 32;
+  Frag<A16> cur, nxt;
+  load_step<A16>(g, mrow, ncol, kq, cur);
+  for (int s = 0; s < steps; ++s) {
+    if (s + 1 < steps) load_step<A16>(g, mrow, ncol, 32 * (s + 1) + kq, nxt);
+    v4i af[D];
+    if (!A16) {
+      const uint4 v = cur.a[0];
+      af[0] = v4i{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
+                  static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
+    } else {
+      uint4 v0 = cur.a[0], v1 = cur.a[D - 1];
+      v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
+      v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
+      // a - 32768 = 256 hi + lo' + 128 with hi = high byte ^ 0x80, lo' = low byte ^ 0x80
+      af[0] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x07050301u)), static_cast<int>(perm(v0.w, v0.z, 0x07050301u)),
+                  static_cast<int>(perm(v1.y, v1.x, 0x07050301u)), static_cast<int>(perm(v1.w, v1.z, 0x07050301u))};
+      af[D - 1] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x06040200u)), static_cast<int>(perm(v0.w, v0.z, 0x06040200u)),
+                      static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (p >= g.nplanes) break;
+        const uint4 b = cur.b[p];
+        acc[p][d] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+            af[d], v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)},
+            acc[p][d], 0, 0, 0);
+      }
+      if (g.ones) one[d] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[d], ones, one[d], 0, 0, 0);
+    }
+    // every 64 k (and after the last step): int32 sums into the int64 accumulators
+    if ((s & 1) || s + 1 == steps) {
+      const int grp = (32 * s) >> g.gshift;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (p >= g.nplanes) break;
+        const long long mlt = MODE == 0 ? g.mult[(static_cast<size_t>(p) * g.G + grp) * g.Np + ncol] : g.cm[p];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int v = A16 ? 256 * acc[p][0][j] + acc[p][D - 1][j] : acc[p][0][j];
+          acc64[j] += static_cast<long long>(v) * mlt;
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[p][d] = v16i{};
+      }
+      if (g.ones) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int v = A16 ? 256 * one[0][j] + one[D - 1][j] : one[0][j];
+          acc64[j] += static_cast<long long>(v) * g.ones;
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) one[d] = v16i{};
+      }
+    }
+    if (s + 1 < steps) cur = nxt;
+  }
+
+  // ---- epilogue: lane holds rows m0 + 8 (j / 4) + 4 (lane / 32) + j % 4 of column ncol
+  const bool col_ok = ncol < g.N;
+  const long long corr = g.corr[ncol];
+  double alpha = 0.0, beta = 0.0, mex = 0.0, absb = 0.0;
+  if (MODE == 0) {
+    alpha = g.alpha_e[ncol];
+    beta = g.beta[ncol];
+    mex = g.margin_exact[ncol];
+    absb = g.absb[ncol];
+  }
+  __syncthreads();  // fix_cnt initialised
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int m = m0 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+    if (m >= g.M || !col_ok) continue;
+    const long long Dv = acc64[j] + corr;
+    const size_t idx = static_cast<size_t>(m) * g.N + ncol;
+    if (MODE == 1) {
+      static_cast<long long *>(g.out)[idx] = Dv;
+    } else if (MODE == 2) {
+      store_out(g, idx, apply_contract(g, Dv, ncol));
+    } else {
+      const double u = static_cast<double>(Dv) * alpha;
+      const double tv = u + beta;
+      const double fl = floor(tv);
+      const double slack = mex + 0x1p-48 * (fabs(u) + fabs(tv) + absb);
+      const double qmaxd = static_cast<double>(g.out_qmax);
+      const bool near = fabs((tv - fl) - 0.5) <= slack;
+      const bool amb = near && fmin(fmax(fl, 0.0), qmaxd) != fmin(fmax(fl + 1.0, 0.0), qmaxd);
+      if (!amb) {
+        store_out(g, idx, static_cast<int>(fmin(fmax(rint(tv), 0.0), qmaxd)));
+      } else {
+        const int slot = atomicAdd(&fix_cnt, 1);
+        if (slot < kExFixCap) fix_list[slot] = (static_cast<uint32_t>(m - blockIdx.y * kExTile) << 16) |
+                                               static_cast<uint32_t>(ncol - blockIdx.x * kExTile);
+      }
+    }
+  }
+  if (MODE == 0) {
+    __syncthreads();
+    const int cnt = fix_cnt;
+    if (cnt == 0) return;
+    // listed outputs: one wave each; beyond the list's capacity a second sweep recomputes the
+    // tile's ambiguous outputs that were not listed
+    for (int e = wave; e < min(cnt, kExFixCap); e += kExThreads / 64) {
+      const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);
+      emulate_one<A16>(g, blockIdx.y * kExTile + static_cast<int>(v >> 16),
+                       blockIdx.x * kExTile + static_cast<int>(v & 0xFFFFu), lane);
+    }
+    if (cnt > kExFixCap) {
+      __syncthreads();
+      // recompute every ambiguous output of this wave's block again, wave-cooperatively
+      for (int j = 0; j < 16; ++j) {
+        for (int src = 0; src < 64; ++src) {
+          const int m = m0 + 8 * (j >> 2) + 4 * (src >> 5) + (j & 3);
+          const int n = n0 + (src & 31);
+          const long long Dv = __shfl(acc64[j], src, 64) + g.corr[n < g.Np ? n : 0];
+          if (m >= g.M || n >= g.N) continue;
+          const double u = static_cast<double>(Dv) * g.alpha_e[n];
+          const double tv = u + g.beta[n];
+          const double fl = floor(tv);
+          const double slack = g.margin_exact[n] + 0x1p-48 * (fabs(u) + fabs(tv) + g.absb[n]);
+          const double qmaxd = static_cast<double>(g.out_qmax);
+          const bool amb = fabs((tv - fl) - 0.5) <= slack &&
+                           fmin(fmax(fl, 0.0), qmaxd) != fmin(fmax(fl + 1.0, 0.0), qmaxd);
+          if (amb) emulate_one<A16>(g, m, n, lane);
+        }
+      }
+    }
+  }
+}
+
+template <bool A16, int MODE>
+qh_status launch(const ExactArgs &g, hipStream_t stream) {
+  const dim3 grid((g.N + kExTile - 1) / kExTile, (g.M + kExTile - 1) / kExTile);
+  hipLaunchKernelGGL((qmm_exact_kernel<A16, MODE>), grid, dim3(kExThreads), 0, stream, g);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "qmm_exact_kernel launch");
+  return QH_STATUS_OK;
+}
+
+template <int MODE>
+qh_status dispatch(const ExactArgs &g, bool a16, hipStream_t stream) {
+  return a16 ? launch<true, MODE>(g, stream) : launch<false, MODE>(g, stream);
+}
+
+}  // namespace
+
+qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, void *out, int mode, int contract,
+                           int divisor, hipStream_t stream) {
+  const QmmShape &sh = p->shape;
+  const QmmDevice &Dv = p->dev;
+  if (m > 65535 * kExTile) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "M=%d too large for one launch", m);
+  ExactArgs g{};
+  g.act = static_cast<const uint8_t *>(act);
+  g.out = out;
+  g.tiles = Dv.tiles;
+  g.KT = sh.Kp / kBK;
+  g.layout_planes = sh.layout_planes;
+  g.M = m;
+  g.N = sh.N;
+  g.K = sh.K;
+  g.Np = sh.Np;
+  g.act_zp = sh.act_zp;
+  g.out_zp = sh.out_zp;
+  g.out_qmax = (1 << sh.out_bits) - 1;
+  g.out16 = sh.out_bits == 16;
+  g.sA = sh.act_scale;
+  g.sO = sh.out_scale;
+  g.contract = contract;
+  g.divisor = divisor;
+  g.bias_q = Dv.bias_q;
+  if (mode == 0) {
+    // requantisation of a per-group weight: planes q and r with their group multipliers
+    g.nplanes = 2;
+    g.ones = 0;
+    g.mult = Dv.mult;
+    g.G = sh.groups;
+    g.gshift = sh.group_shift;
+    g.corr = Dv.corr_rq;
+    g.alpha_e = Dv.alpha_e;
+    g.beta = Dv.beta;
+    g.margin_exact = Dv.margin_exact;
+    g.absb = Dv.absb;
+    g.s32g = Dv.s32g;
+    g.bias_deq = Dv.bias_deq;
+  } else {
+    // the integer dot product sum_k (a - zp) w_int
+    g.nplanes = sh.int_planes;
+    g.cm[0] = sh.int_mult[0];
+    g.cm[1] = sh.int_mult[1];
+    g.ones = sh.int_ones;
+    g.G = 1;
+    g.gshift = 6;
+    g.corr = Dv.corr_int;
+  }
+  const bool a16 = sh.act_bits == 16;
+  if (mode == 0) return dispatch<0>(g, a16, stream);
+  if (mode == 1) return dispatch<1>(g, a16, stream);
+  return dispatch<2>(g, a16, stream);
+}
+
+}  // namespace qh

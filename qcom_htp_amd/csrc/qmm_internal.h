@@ -82,6 +82,13 @@ struct QmmDevice {
   double *gemv_margin_r1; // 16-bit acts GEMV: per-channel coefficient of R1[m] in the margin
   int8_t *resid;    // 8-bit acts: rounding residues r[n][k] (fl32(w s32) = 2^E (w M + r)), [N][K],
                     // read by the GEMM's exact fixup (|r| <= 64)
+  int32_t *bias_q;  // [Np] the descriptor's int32 bias (integer contracts)
+  int64_t *corr_int; // [Np] activation-shift term of the exact integer dot product sum (a - zp) w_int
+  // Per-group weights (exact integer GEMM): multipliers of the code and residue planes per
+  // (plane, group, channel) [2][G][Np], the shift term of that sum, and the float32 group scales
+  int64_t *mult;
+  int64_t *corr_rq;
+  float *s32g;      // [N][G]
 };
 
 struct QmmShape {
@@ -96,6 +103,35 @@ struct QmmShape {
   int act_zp, out_zp;
   double act_scale, out_scale;
   int epi_clamp;      // GEMM epilogue must clamp t before rounding (|t| < 2^30 not proven)
+  // Exact integer GEMM (qmm_exact.hip): weight planes per 32 channels in the tile layout (1, or 2
+  // for 16-bit acts and the exact-only formats), the planes / multipliers / all-ones multiplier
+  // of the integer dot product, and the per-group scale groups.
+  int layout_planes;
+  int exact_only;     // per-group / int16 weights: no GEMM / GEMV state
+  int int_planes;
+  long long int_mult[2];
+  int int_ones;
+  int groups, group_shift;
+};
+
+// Arguments of the exact integer GEMM (qmm_exact.hip).
+struct ExactArgs {
+  const uint8_t *act;
+  void *out;
+  const uint8_t *tiles;
+  int KT, layout_planes;
+  int M, N, K, Np;
+  int nplanes, ones;
+  long long cm[2];
+  const int64_t *mult;
+  int G, gshift;
+  const int64_t *corr;
+  const double *alpha_e, *beta, *margin_exact, *absb, *bias_deq;
+  const float *s32g;
+  double sA, sO;
+  int act_zp, out_zp, out_qmax, out16;
+  int contract, divisor;
+  const int32_t *bias_q;
 };
 
 }  // namespace qh
@@ -120,6 +156,9 @@ qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void
 bool gemv_fits(const qh_qmm_prepared *p, int m);  // the GEMV's LDS staging holds M x K
 qh_status launch_qmm_accumulate(const qh_qmm_prepared *p, int m, const void *act, int64_t *acc,
                                 hipStream_t stream);
+// mode 0: requantised output (per-group weights), 1: int64 accumulators, 2: integer contract
+qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, void *out, int mode, int contract,
+                           int divisor, hipStream_t stream);
 qh_status launch_gdn_solve_f32(const float *A, float *T, int heads, int C, int precision, hipStream_t stream);
 qh_status launch_gdn_solve_u16(const uint16_t *A, uint16_t *T, int heads, int C, int zpA, int zpT, float sA,
                                float sT, int precision, hipStream_t stream);

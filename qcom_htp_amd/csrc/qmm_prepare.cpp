@@ -77,6 +77,180 @@ struct TileWriter {
   }
 };
 
+// Prepared state of the formats that run on the exact integer GEMM only (qmm_exact.hip):
+//   * QH_WEIGHT_I4_GROUP: the oracle's weight fl32(q s_g) = 2^E_g (q M_g + r) (s_g = M_g 2^E_g);
+//     with E_min = min_g E_g and d_g = E_g - E_min the dot product is 2^E_min D exactly, where
+//     D = sum_g [M_g 2^d_g sum_{k in g} (a - zp) q + 2^d_g sum_{k in g} (a - zp) r].  Plane 0
+//     holds q, plane 1 holds r (|r| <= 64), with those multipliers per (group, channel).
+//   * QH_WEIGHT_I16: q16 = 256 hi + lo' + 128 (hi = q16 >> 8, lo' = (q16 & 255) - 128): planes hi
+//     (x 256) and lo' (x 1) plus 128 times the activation row sum (the all-ones plane).
+qh_status prepare_exact(const qh_qmm_desc *d, qh_qmm_prepared **out) {
+  const bool group = d->weight_format == QH_WEIGHT_I4_GROUP;
+  const int N = static_cast<int>(d->n), K = static_cast<int>(d->k);
+  const bool a16 = d->act_bits == 16;
+  int gsz = 64, gshift = 6;
+  if (group) {
+    if (d->weight_nk == nullptr || d->group_scale == nullptr)
+      return fail(QH_STATUS_INVALID_ARGUMENT, "per-group weights need weight_nk and group_scale");
+    gsz = static_cast<int>(d->group_size);
+    if (gsz < 64 || (gsz & (gsz - 1)) || K % gsz)
+      return fail(QH_STATUS_SHAPE_UNSUPPORTED, "group_size=%d must be a power of two >= 64 dividing K=%d", gsz, K);
+    gshift = 0;
+    while ((1 << gshift) < gsz) ++gshift;
+  } else if (d->weight16_nk == nullptr) {
+    return fail(QH_STATUS_INVALID_ARGUMENT, "QH_WEIGHT_I16 needs weight16_nk");
+  }
+  const int G = group ? K / gsz : 1;
+  QmmShape sh{};
+  sh.N = N;
+  sh.K = K;
+  sh.Kp = round_up(K, kBK);
+  sh.act_bits = static_cast<int>(d->act_bits);
+  sh.out_bits = static_cast<int>(d->out_bits);
+  sh.wfmt = static_cast<int>(d->weight_format);
+  sh.act_zp = d->act_zp;
+  sh.out_zp = d->out_zp;
+  sh.act_scale = d->act_scale;
+  sh.out_scale = d->out_scale;
+  sh.ncols_op = round_up(2 * N, kBN);
+  sh.Np = sh.ncols_op / 2;
+  sh.layout_planes = 2;
+  sh.exact_only = 1;
+  sh.groups = G;
+  sh.group_shift = gshift;
+  const int Np = sh.Np, KT = sh.Kp / kBK;
+  const int64_t c = (a16 ? 32896 : 128) - d->act_zp;  // activation shift of the exact GEMM
+  const double amax = static_cast<double>(std::max(d->act_zp, (1 << d->act_bits) - 1 - d->act_zp));
+
+  std::vector<uint8_t> tiles(static_cast<size_t>(sh.ncols_op) * sh.Kp, 0);
+  TileWriter tw{tiles, KT};
+  std::vector<int64_t> corr_int(Np, 0), corr_rq(Np, 0), mult;
+  std::vector<int32_t> biasv(Np, 0);
+  std::vector<double> alpha_e(Np, 0.0), beta(Np, 0.0), margin_exact(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0);
+  std::vector<float> s32g;
+  for (int n = 0; n < N; ++n) biasv[n] = d->bias_q ? d->bias_q[n] : 0;
+  if (!group) {
+    sh.int_planes = 2;
+    sh.int_mult[0] = 256;
+    sh.int_mult[1] = 1;
+    sh.int_ones = 128;
+    for (int n = 0; n < N; ++n) {
+      const int cq = (n / 32) * 64 + (n % 32);
+      int64_t cs = 0;
+      for (int k = 0; k < K; ++k) {
+        const int q = d->weight16_nk[static_cast<size_t>(n) * K + k];
+        tw.put(cq, k, q >> 8);                 // arithmetic: hi in [-128, 127]
+        tw.put(cq + 32, k, (q & 255) - 128);   // lo' in [-128, 127]
+        cs += q;
+      }
+      corr_int[n] = c * cs;
+    }
+  } else {
+    sh.int_planes = 1;
+    sh.int_mult[0] = 1;
+    sh.int_mult[1] = 0;
+    sh.int_ones = 0;
+    mult.assign(static_cast<size_t>(2) * G * Np, 0);
+    s32g.assign(static_cast<size_t>(N) * G, 1.0f);
+    const double sA = d->act_scale, sO = d->out_scale;
+    std::vector<int64_t> Mg(G);
+    std::vector<int> Eg(G);
+    std::vector<char> live(G);
+    for (int n = 0; n < N; ++n) {
+      // the common exponent comes from the groups with a nonzero code: an all-zero group adds
+      // exactly nothing whatever its scale (e.g. the epsilon scale of an all-zero weight block)
+      int emin = std::numeric_limits<int>::max();
+      for (int g = 0; g < G; ++g) {
+        const float sg = d->group_scale[static_cast<size_t>(n) * G + g];
+        if (!(sg > 0.0f) || !std::isfinite(sg) || sg < std::numeric_limits<float>::min())
+          return fail(QH_STATUS_INVALID_ARGUMENT, "group_scale[%d][%d] must be a positive normal float", n, g);
+        split_float(sg, &Mg[g], &Eg[g]);
+        s32g[static_cast<size_t>(n) * G + g] = sg;
+        live[g] = 0;
+        for (int k = g * gsz; k < (g + 1) * gsz; ++k) live[g] |= d->weight_nk[static_cast<size_t>(n) * K + k] != 0;
+        if (live[g]) emin = std::min(emin, Eg[g]);
+      }
+      if (emin == std::numeric_limits<int>::max()) emin = Eg[0];
+      const int cq = (n / 32) * 64 + (n % 32);
+      int64_t csq = 0;
+      double sum_abs = 0.0;  // sum_k 2^d_g |q M_g + r|: bounds D and the oracle's float noise
+      double corr_d = 0.0;
+      int64_t corr_acc = 0;
+      for (int g = 0; g < G; ++g) {
+        const int dg = live[g] ? Eg[g] - emin : 0;
+        if (dg > 30) return fail(QH_STATUS_UNSUPPORTED, "channel %d: group scales span more than 2^30", n);
+        const int64_t m0 = live[g] ? Mg[g] << dg : 0, m1 = live[g] ? int64_t{1} << dg : 0;
+        mult[(static_cast<size_t>(0) * G + g) * Np + n] = m0;
+        mult[(static_cast<size_t>(1) * G + g) * Np + n] = m1;
+        int64_t sq = 0, sr = 0;
+        const float sg = s32g[static_cast<size_t>(n) * G + g];
+        for (int k = g * gsz; k < (g + 1) * gsz; ++k) {
+          const int q = d->weight_nk[static_cast<size_t>(n) * K + k];
+          if (q < -127 || q > 127)
+            return fail(QH_STATUS_INVALID_ARGUMENT, "weight code %d at (n=%d,k=%d) outside [-127,127]", q, n, k);
+          const float wd = static_cast<float>(q) * sg;  // the oracle's float32 weight
+          const double wp = std::ldexp(static_cast<double>(wd), -Eg[g]);
+          const int64_t Wp = static_cast<int64_t>(wp);
+          if (static_cast<double>(Wp) != wp) return fail(QH_STATUS_RUNTIME_ERROR, "internal: non-integer weight at n=%d", n);
+          const int64_t r = Wp - static_cast<int64_t>(q) * Mg[g];
+          if (r < -127 || r > 127) return fail(QH_STATUS_RUNTIME_ERROR, "internal: residue %lld out of int8", (long long)r);
+          tw.put(cq, k, q);
+          tw.put(cq + 32, k, static_cast<int>(r));
+          sq += q;
+          sr += r;
+          sum_abs += std::ldexp(std::fabs(static_cast<double>(Wp)), dg);
+        }
+        csq += sq;
+        corr_acc += m0 * sq + m1 * sr;
+        corr_d += static_cast<double>(m0) * static_cast<double>(sq) + static_cast<double>(m1) * static_cast<double>(sr);
+      }
+      // D = sum of int64 terms; every partial sum is bounded by amax * sum_abs + |c corr|
+      const double bound = amax * sum_abs + std::fabs(static_cast<double>(c) * corr_d);
+      if (!(bound < 0x1p62))
+        return fail(QH_STATUS_UNSUPPORTED, "channel %d: per-group exact sum exceeds int64 (group scales span too far)", n);
+      corr_rq[n] = c * corr_acc;
+      corr_int[n] = c * csq;
+      const double ae = std::ldexp(sA, emin) / sO;
+      alpha_e[n] = ae;
+      bdeq[n] = d->bias_float ? static_cast<double>(d->bias_float[n]) : 0.0;
+      beta[n] = bdeq[n] / sO + d->out_zp;
+      absb[n] = 2.0 * std::fabs(beta[n]) + 2.0 * d->out_zp + 1.0;
+      // the oracle's float64 noise: K roundings of terms bounded by amax 2^E_min sum_abs / K
+      margin_exact[n] = (K + 8.0) * std::ldexp(1.0, -52) * amax * sum_abs * ae * kSafety;
+    }
+  }
+  auto *p = new qh_qmm_prepared();
+  p->shape = sh;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  p->device_id = dev;
+  DevAlloc al;
+  qh_status st = QH_STATUS_OK;
+  QmmDevice &D = p->dev;
+  std::memset(&D, 0, sizeof(D));
+  if (st == QH_STATUS_OK) st = al.upload(&D.tiles, tiles);
+  if (st == QH_STATUS_OK) st = al.upload(&D.bias_q, biasv);
+  if (st == QH_STATUS_OK) st = al.upload(&D.corr_int, corr_int);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.mult, mult);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.corr_rq, corr_rq);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.s32g, s32g);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.alpha_e, alpha_e);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.beta, beta);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.margin_exact, margin_exact);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.absb, absb);
+  if (st == QH_STATUS_OK && group) st = al.upload(&D.bias_deq, bdeq);
+  if (st != QH_STATUS_OK) {
+    al.release();
+    delete p;
+    return st;
+  }
+  p->device_bytes = al.bytes;
+  p->gemm_weight_bytes = tiles.size();
+  p->gemv_weight_bytes = 0;
+  *out = p;
+  return QH_STATUS_OK;
+}
+
 }  // namespace
 }  // namespace qh
 
@@ -90,12 +264,21 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     return fail(QH_STATUS_UNSUPPORTED, "act_bits must be 8 or 16 (got %u)", d->act_bits);
   if (d->out_bits != 8 && d->out_bits != 16)
     return fail(QH_STATUS_UNSUPPORTED, "out_bits must be 8 or 16 (got %u)", d->out_bits);
-  if (d->weight_format > QH_WEIGHT_I4_LPBQ)
+  if (d->weight_format > QH_WEIGHT_I16)
     return fail(QH_STATUS_UNSUPPORTED, "unknown weight_format %u", d->weight_format);
   if (d->k == 0 || d->n == 0 || d->k % 32 || d->n % 32)
     return fail(QH_STATUS_SHAPE_UNSUPPORTED, "K and N must be positive multiples of 32 (K=%u N=%u)", d->k, d->n);
   if (d->k > 65536 || d->n > (1u << 20))
     return fail(QH_STATUS_SHAPE_UNSUPPORTED, "K <= 65536 and N <= 2^20 required (K=%u N=%u)", d->k, d->n);
+  {
+    const int act_qmax = (1 << d->act_bits) - 1, out_qmax = (1 << d->out_bits) - 1;
+    if (d->act_zp < 0 || d->act_zp > act_qmax || d->out_zp < 0 || d->out_zp > out_qmax)
+      return fail(QH_STATUS_INVALID_ARGUMENT, "zero point out of range (act_zp=%d out_zp=%d)", d->act_zp, d->out_zp);
+    if (!(d->act_scale > 0.0) || !(d->out_scale > 0.0) || !std::isfinite(d->act_scale) || !std::isfinite(d->out_scale))
+      return fail(QH_STATUS_INVALID_ARGUMENT, "act_scale and out_scale must be finite and > 0");
+  }
+  if (d->weight_format == QH_WEIGHT_I4_GROUP || d->weight_format == QH_WEIGHT_I16) return prepare_exact(d, out);
+  const int act_qmax = (1 << d->act_bits) - 1;
   const bool lpbq = d->weight_format == QH_WEIGHT_I4_LPBQ;
   if (lpbq && d->lpbq_block != 32 && d->lpbq_block != 64)
     return fail(QH_STATUS_UNSUPPORTED, "lpbq_block must be 32 or 64 (got %u)", d->lpbq_block);
@@ -103,11 +286,6 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     return fail(QH_STATUS_SHAPE_UNSUPPORTED, "K=%u must be a multiple of lpbq_block=%u", d->k, d->lpbq_block);
   if (d->weight_nk == nullptr || d->weight_scale == nullptr || (lpbq && d->lpbq_block_scale == nullptr))
     return fail(QH_STATUS_INVALID_ARGUMENT, "weight_nk / weight_scale / lpbq_block_scale is NULL");
-  const int act_qmax = (1 << d->act_bits) - 1, out_qmax = (1 << d->out_bits) - 1;
-  if (d->act_zp < 0 || d->act_zp > act_qmax || d->out_zp < 0 || d->out_zp > out_qmax)
-    return fail(QH_STATUS_INVALID_ARGUMENT, "zero point out of range (act_zp=%d out_zp=%d)", d->act_zp, d->out_zp);
-  if (!(d->act_scale > 0.0) || !(d->out_scale > 0.0) || !std::isfinite(d->act_scale) || !std::isfinite(d->out_scale))
-    return fail(QH_STATUS_INVALID_ARGUMENT, "act_scale and out_scale must be finite and > 0");
 
   const int N = static_cast<int>(d->n), K = static_cast<int>(d->k);
   const int wq_max = d->weight_format == QH_WEIGHT_I8 ? 127 : 7;
@@ -192,6 +370,13 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     sh.Np = sh.ncols_op / 2;
   }
   sh.gemv_fmt = d->weight_format == QH_WEIGHT_I8 ? kTileI8 : kTileI4;
+  sh.layout_planes = a16 ? 2 : 1;
+  sh.int_planes = 1;
+  sh.int_mult[0] = 1;
+  sh.int_mult[1] = 0;
+  sh.int_ones = 0;
+  sh.groups = 1;
+  sh.group_shift = 6;
   const int KT = sh.Kp / kBK;
 
   // ---- GEMM operand tiles ------------------------------------------------------------------
@@ -250,6 +435,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   std::vector<double> margin_exact(Np, 0.0);
   std::vector<int32_t> scale_exp(Np, 0);
   std::vector<float> s32v(Np, 1.0f);
+  std::vector<int32_t> biasv(Np, 0);
+  std::vector<int64_t> corr_int(Np, 0);
   const double a_base = a16 ? 32768.0 : 128.0;  // the kernels shift activations by this
   for (int n = 0; n < N; ++n) {
     const float s = d->weight_scale[n];
@@ -287,6 +474,9 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     scale_exp[n] = expo[n];
     margin_exact[n] = inv_sO * sA * two_e * noise * kSafety;
     s32v[n] = s;
+    biasv[n] = d->bias_q ? d->bias_q[n] : 0;
+    // the exact integer GEMM shifts activations by 128 (8-bit) or 32896 (16-bit, 256 hi + lo')
+    corr_int[n] = static_cast<int64_t>((a16 ? 32896 : 128) - d->act_zp) * colsum_q[n];
   }
 
   // ---- upload -------------------------------------------------------------------------------
@@ -317,6 +507,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.margin_exact, margin_exact);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
   if (st == QH_STATUS_OK && !a16) st = al.upload(&D.resid, resid);
+  if (st == QH_STATUS_OK) st = al.upload(&D.bias_q, biasv);
+  if (st == QH_STATUS_OK) st = al.upload(&D.corr_int, corr_int);
   if (st != QH_STATUS_OK) {
     al.release();
     delete p;

@@ -22,15 +22,27 @@ from .cases import FAMILIES, Family, QmmCase
 
 PATH_AUTO, PATH_GEMM, PATH_GEMV = 0, 1, 2
 
-__all__ = ["QuantMatmul", "PATH_AUTO", "PATH_GEMM", "PATH_GEMV", "weight_format_of"]
+__all__ = ["QuantMatmul", "PATH_AUTO", "PATH_GEMM", "PATH_GEMV", "CONTRACTS", "weight_format_of"]
 
 
 def weight_format_of(family: Family) -> int:
     if family.weight_schema == "lpbq_blockwise_expansion":
         return _lib.QH_WEIGHT_I4_LPBQ
+    if family.weight_schema == "per_group":
+        return _lib.QH_WEIGHT_I4_GROUP
     if family.weight_schema != "per_output_channel":
         raise ValueError(f"{family.name}: weight schema {family.weight_schema!r} is not supported")
     return _lib.QH_WEIGHT_I8 if family.weight_bits == 8 else _lib.QH_WEIGHT_I4
+
+
+# Integer output contracts of qh_qmm_run_contract (see include/qhtp.h).
+CONTRACTS = {
+    "clip_i32": _lib.QH_CONTRACT_CLIP_I32,
+    "clip_i64": _lib.QH_CONTRACT_CLIP_I64,
+    "div_rint": _lib.QH_CONTRACT_DIV_RINT,
+    "floor256_div_rint": _lib.QH_CONTRACT_FLOOR256_DIV_RINT,
+    "round_div": _lib.QH_CONTRACT_ROUND_DIV,
+}
 
 
 def _stream_ptr(stream: Optional[torch.cuda.Stream]) -> int:
@@ -42,8 +54,10 @@ class QuantMatmul:
     """out[M,N] = clip(rint(((act - act_zp) sA) @ fl32(w_int s32).T + bias_deq) / sO + out_zp)).
 
     Parameters mirror the reference case (``case.json`` qparams): ``weight_q_nk`` int codes
-    [N,K]; ``weight_scale`` float32 [N]; ``bias_q`` int32 [N]; ``lpbq_block_scale`` uint8
-    [N, K/block] for LPBQ; activation/output bit widths, scales and zero points.
+    [N,K] (int16 for ``QH_WEIGHT_I16``); ``weight_scale`` float32 [N], or [N, K/group] group
+    scales for the per-group schema; ``bias_q`` int32 [N] (``bias_float`` float32 [N] for the
+    per-group schema); ``lpbq_block_scale`` uint8 [N, K/block] for LPBQ; activation/output bit
+    widths, scales and zero points.
     """
 
     def __init__(
@@ -61,12 +75,23 @@ class QuantMatmul:
         weight_format: int,
         lpbq_block_scale: Optional[np.ndarray] = None,
         lpbq_block: int = 0,
+        bias_float: Optional[np.ndarray] = None,
         device: Optional[torch.device] = None,
     ):
-        w = np.ascontiguousarray(weight_q_nk, dtype=np.int8)
+        i16 = weight_format == _lib.QH_WEIGHT_I16
+        group = weight_format == _lib.QH_WEIGHT_I4_GROUP
+        w = np.ascontiguousarray(weight_q_nk, dtype=np.int16 if i16 else np.int8)
         n, k = w.shape
-        s32 = np.ascontiguousarray(weight_scale, dtype=np.float32).reshape(n)
+        if group:
+            gs = np.ascontiguousarray(weight_scale, dtype=np.float32)
+            if gs.ndim != 2 or gs.shape[0] != n or k % gs.shape[1]:
+                raise ValueError("per-group weight_scale must be [N, K / group_size]")
+            s32 = None
+        else:
+            gs = None
+            s32 = None if weight_scale is None else np.ascontiguousarray(weight_scale, dtype=np.float32).reshape(n)
         b = None if bias_q is None else np.ascontiguousarray(bias_q, dtype=np.int32).reshape(n)
+        bf = None if bias_float is None else np.ascontiguousarray(bias_float, dtype=np.float32).reshape(n)
         blk = None
         if weight_format == _lib.QH_WEIGHT_I4_LPBQ:
             if lpbq_block_scale is None or lpbq_block not in (32, 64):
@@ -88,10 +113,14 @@ class QuantMatmul:
             out_zp=int(out_zp),
             act_scale=float(act_scale),
             out_scale=float(out_scale),
-            weight_nk=w.ctypes.data,
+            weight_nk=None if i16 else w.ctypes.data,
             lpbq_block_scale=blk.ctypes.data if blk is not None else None,
-            weight_scale=s32.ctypes.data,
+            weight_scale=s32.ctypes.data if s32 is not None else None,
             bias_q=b.ctypes.data if b is not None else None,
+            group_scale=gs.ctypes.data if gs is not None else None,
+            group_size=k // gs.shape[1] if gs is not None else 0,
+            bias_float=bf.ctypes.data if bf is not None else None,
+            weight16_nk=w.ctypes.data if i16 else None,
         )
         handle = C.c_void_p()
         L = _lib.lib()
@@ -120,6 +149,7 @@ class QuantMatmul:
             weight_format=fmt,
             lpbq_block_scale=case.lpbq_block_int_scale,
             lpbq_block=fam.lpbq_block_size if fmt == _lib.QH_WEIGHT_I4_LPBQ else 0,
+            bias_float=getattr(case, "bias_float", None),
             device=device,
         )
 
@@ -151,6 +181,21 @@ class QuantMatmul:
         st = _lib.lib().qh_qmm_accumulate(self._h, m, act.data_ptr(), acc.data_ptr(), _stream_ptr(stream))
         _lib.check(st, "qh_qmm_accumulate")
         return acc
+
+    def run_contract(self, act: torch.Tensor, contract, divisor: int = 1, out: Optional[torch.Tensor] = None,
+                     stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """One of the reference's integer output contracts (``CONTRACTS`` name or id) applied to
+        the exact integer dot product sum_k (act - act_zp) * w_int."""
+        m = self._check_act(act)
+        cid = CONTRACTS[contract] if isinstance(contract, str) else int(contract)
+        if out is None:
+            out = torch.empty((m, self.n), dtype=self.out_dtype, device=act.device)
+        elif out.shape != (m, self.n) or out.dtype != self.out_dtype or not out.is_contiguous():
+            raise ValueError("bad output tensor")
+        st = _lib.lib().qh_qmm_run_contract(self._h, m, act.data_ptr(), out.data_ptr(), cid, int(divisor),
+                                            _stream_ptr(stream))
+        _lib.check(st, "qh_qmm_run_contract")
+        return out
 
     def close(self) -> None:
         if getattr(self, "_h", None) and self._h.value:

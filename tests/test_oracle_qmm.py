@@ -47,7 +47,7 @@ def test_seed_and_weight_quantizer_match_golden(key):
         np.testing.assert_array_equal(wq["expanded"], SMALL[key + "/weight_lpbq_expanded_q_nk"])
 
 
-@pytest.mark.parametrize("key", GATED_KEYS)
+@pytest.mark.parametrize("key", ALL_KEYS)
 def test_case_and_oracle_match_golden_small(key):
     fam, case = key.split("/")
     c = C.make_case(fam, case, 32, 128, 32)
@@ -66,11 +66,12 @@ def test_case_and_oracle_match_golden_small(key):
     g = SMALL[key + "/output_q"]
     assert out.dtype == g.dtype
     np.testing.assert_array_equal(out, g)
-    qr = qmm.dequantized_output(c.activation_q, c.weight_int_nk, c.weight_scale, c.bias_q, c.act_scale, c.family.act_zp)
+    qr = qmm.dequantized_output(c.activation_q, c.weight_int_nk, c.weight_scale, c.bias_q, c.act_scale, c.family.act_zp,
+                                c.bias_float)
     np.testing.assert_array_equal(qr.astype(np.float32), SMALL[key + "/output_quantized_path_float"])
 
 
-@pytest.mark.parametrize("key", GATED_KEYS)
+@pytest.mark.parametrize("key", ALL_KEYS)
 def test_case_and_oracle_match_golden_256(key):
     fam, case = key.split("/")
     c = C.make_case(fam, case, 256, 256, 256)
@@ -170,3 +171,104 @@ def test_near_tie_stress_covers_both_fixup_regimes(fam):
     f = flagged_per_tile(c, d)
     assert 100 < f[0, 0] < 1024, f
     assert f[1, 0] > 1024, f
+
+
+# ---------------------------------------------------------------------- integer contracts
+
+
+def _rand_acc_case(seed, m=5, k=40, n=7, act_bits=16, wq=7):
+    rng = np.random.default_rng(seed)
+    hi = (1 << act_bits) - 1
+    a = rng.integers(0, hi + 1, size=(m, k)).astype(np.int64)
+    w = rng.integers(-wq, wq + 1, size=(k, n)).astype(np.int64)
+    return a, w
+
+
+def _exact_round_half_even(fr):
+    """Round a Fraction to the nearest integer, ties to even (np.rint's rule)."""
+    from fractions import Fraction
+
+    fl = fr.numerator // fr.denominator
+    rem = fr - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2):
+        return fl + 1
+    return fl
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_contract_legacy_matches_reference_step_and_int32_wrap(seed):
+    a, w = _rand_acc_case(seed, act_bits=16, wq=127)
+    rng = np.random.default_rng(100 + seed)
+    bias = rng.integers(-(1 << 31), (1 << 31), size=w.shape[1]).astype(np.int64)
+    acc = (a - 32768) @ w
+    got = qmm.contract_output(acc, "clip_i32", bias_q=bias, out_bits=16)
+    ref = qmm.reference_step(16, 8, 16, a.astype(np.uint16), w, bias.astype(np.int32), contract="legacy")
+    np.testing.assert_array_equal(got, ref)
+    # Python integers with an explicit two's-complement wrap
+    for i in range(a.shape[0]):
+        for j in range(w.shape[1]):
+            v = sum((int(a[i, k]) - 32768) * int(w[k, j]) for k in range(a.shape[1])) + int(bias[j])
+            v = (v + (1 << 31)) % (1 << 32) - (1 << 31)
+            assert got[i, j] == min(max(v, 0), 65535)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_contract_native_a16_matches_reference_step_and_exact_rounding(seed):
+    from fractions import Fraction
+
+    a, w = _rand_acc_case(seed, k=64, wq=127)
+    acc = (a - 32768) @ w
+    got = qmm.contract_output(acc, "div_rint", divisor=127, out_zp=32768, out_bits=16)
+    ref = qmm.reference_step(16, 8, 16, a.astype(np.uint16), w, None, contract="native", family_name="w8a16")
+    np.testing.assert_array_equal(got, ref)
+    # 127 is odd: acc / 127 + 32768 is never a half-integer, so float64 rounding equals the exact one
+    for (i, j), v in np.ndenumerate(acc):
+        want = min(max(_exact_round_half_even(Fraction(int(v), 127) + 32768), 0), 65535)
+        assert got[i, j] == want
+    a4, w4 = _rand_acc_case(seed + 10, k=64, wq=7)
+    acc4 = (a4 - 32768) @ w4
+    got4 = qmm.contract_output(acc4, "floor256_div_rint", divisor=7, out_zp=32768, out_bits=16)
+    ref4 = qmm.reference_step(16, 4, 16, a4.astype(np.uint16), w4, None, contract="native", family_name="w4a16")
+    np.testing.assert_array_equal(got4, ref4)
+    for (i, j), v in np.ndenumerate(acc4):
+        fl = (int(v) // 256) * 256
+        want = min(max(_exact_round_half_even(Fraction(fl, 7) + 32768), 0), 65535)
+        assert got4[i, j] == want
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_contract_scalar_lpbq_models(seed):
+    a, w = _rand_acc_case(seed, act_bits=16, k=48, wq=7)
+    acc = (a - 32768) @ w
+    got = qmm.contract_output(acc, "round_div", divisor=7, out_zp=32768, out_bits=16)
+    np.testing.assert_array_equal(got, qmm.w4a16_lpbq_scalar_native(a.astype(np.uint16), w))
+    for (i, j), v in np.ndenumerate(acc):  # half away from zero, by hand
+        q = (abs(int(v)) * 2 + 7) // 14
+        q = q if v >= 0 else -q
+        assert got[i, j] == min(max(q + 32768, 0), 65535)
+    a8, w8 = _rand_acc_case(seed + 20, act_bits=8, k=48, wq=7)
+    rng = np.random.default_rng(seed)
+    eff = rng.integers(-20000, 20000, size=w8.shape[1]).astype(np.int64)
+    got8 = qmm.contract_output(a8 @ w8, "clip_i64", bias_q=eff, out_bits=8)
+    np.testing.assert_array_equal(got8, qmm.w4a8_lpbq_scalar(eff, w8, a8.astype(np.uint8)))
+
+
+def test_round_div_ties_and_signs():
+    v = np.array([0, 3, 4, -3, -4, 10, 11, -10, -11, 7 * 5 + 3, -(7 * 5 + 3)], np.int64)
+    np.testing.assert_array_equal(qmm.round_div(v, 7), [0, 0, 1, 0, -1, 1, 2, -1, -2, 5, -5])
+    np.testing.assert_array_equal(qmm.round_div(v, 7), qmm.round_div7(v))
+    np.testing.assert_array_equal(qmm.round_div(np.array([1, 2, 3, -1, -2, -3]), 2), [1, 1, 2, -1, -1, -2])
+
+
+def test_w16a16_split_identity_and_brute_force():
+    rng = np.random.default_rng(0xB17E)
+    x = rng.integers(0, 65536, size=(4, 24)).astype(np.uint16)
+    q16 = rng.integers(-32768, 32768, size=(5, 24)).astype(np.int16)
+    q16[0, :3] = [32767, -32768, 32640]  # the ends of the range
+    hi, lo = qmm.split_int16(q16)
+    assert hi.min() >= -128 and hi.max() <= 127 and lo.min() >= 0 and lo.max() <= 255
+    np.testing.assert_array_equal(hi * 256 + lo, q16.astype(np.int64))
+    acc = qmm.w16a16_accumulator(x, q16, 32768)
+    for i in range(4):
+        for j in range(5):
+            assert acc[i, j] == sum((int(x[i, k]) - 32768) * int(q16[j, k]) for k in range(24))
