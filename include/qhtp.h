@@ -160,6 +160,20 @@ typedef enum qh_contract {
 qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
                               uint32_t contract, uint32_t divisor, void *stream);
 
+/* `contract` value of qh_qmm_run_chain that selects the float-derived requantisation of
+ * qh_qmm_run instead of an integer contract. */
+#define QH_CONTRACT_NONE 0xFFFFFFFFu
+
+/* A chain of `chain` identical matmuls, each one's output the next one's activation (the
+ * reference's CHAIN graphs: gen_quant_chain.py:1346-1361, HmPreparedRun.chain of
+ * handwritten_hmx_matmul.h:32; reference output = the step applied chain times, :1542-1544).
+ * Needs K == N and act_bits == out_bits when chain > 1.  Each step is qh_qmm_run
+ * (contract = QH_CONTRACT_NONE) or qh_qmm_run_contract(contract, divisor).  Intermediate results
+ * alternate between out_dev and scratch_dev (the op's scratch operand: M x N output elements;
+ * NULL allowed when chain == 1), so the last one lands in out_dev.  act_dev is only read. */
+qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t chain, const void *act_dev,
+                           void *out_dev, void *scratch_dev, uint32_t contract, uint32_t divisor, void *stream);
+
 typedef struct qh_qmm_info {
   uint32_t k, n, act_bits, out_bits, weight_format, lpbq_block;
   uint64_t device_bytes;      /* device memory held by the prepared state */

@@ -30,6 +30,7 @@ QH_CONTRACT_CLIP_I64 = 1
 QH_CONTRACT_DIV_RINT = 2
 QH_CONTRACT_FLOOR256_DIV_RINT = 3
 QH_CONTRACT_ROUND_DIV = 4
+QH_CONTRACT_NONE = 0xFFFFFFFF
 
 # Packed weight carriers (qh_weight_carrier) and their flags.
 CARRIERS = {
@@ -65,6 +66,7 @@ EXPORTED = (
     "qh_qmm_run_path",
     "qh_qmm_accumulate",
     "qh_qmm_run_contract",
+    "qh_qmm_run_chain",
     "qh_qmm_query",
     "qh_qmm_release",
     "qh_weight_unpack",
@@ -147,6 +149,8 @@ def _declare(L: C.CDLL) -> None:
     L.qh_qmm_accumulate.restype = st
     L.qh_qmm_run_contract.argtypes = [vp, u32, vp, vp, u32, u32, vp]
     L.qh_qmm_run_contract.restype = st
+    L.qh_qmm_run_chain.argtypes = [vp, u32, u32, vp, vp, vp, u32, u32, vp]
+    L.qh_qmm_run_chain.restype = st
     L.qh_qmm_query.argtypes = [vp, C.POINTER(QmmInfo)]
     L.qh_qmm_query.restype = st
     L.qh_qmm_release.argtypes = [vp]

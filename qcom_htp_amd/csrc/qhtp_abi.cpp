@@ -112,6 +112,34 @@ qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const voi
                           divides ? static_cast<int>(divisor) : 1, static_cast<hipStream_t>(stream));
 }
 
+qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t chain, const void *act_dev,
+                           void *out_dev, void *scratch_dev, uint32_t contract, uint32_t divisor, void *stream) {
+  if (prep == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: prepared handle is NULL");
+  if (chain == 0 || chain > 4096) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: chain=%u", chain);
+  if (act_dev == nullptr || out_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: NULL buffer");
+  const QmmShape &sh = prep->shape;
+  if (chain > 1) {
+    if (sh.K != sh.N || sh.act_bits != sh.out_bits)
+      return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_qmm_run_chain: chain > 1 needs K == N and act_bits == out_bits");
+    if (scratch_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: chain > 1 needs scratch");
+    if (reinterpret_cast<uintptr_t>(out_dev) % 16 || reinterpret_cast<uintptr_t>(scratch_dev) % 16)
+      return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: out and scratch must be 16-byte aligned");
+    if (scratch_dev == out_dev || scratch_dev == act_dev || out_dev == act_dev)
+      return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: act, out and scratch must be distinct");
+  }
+  const void *src = act_dev;
+  for (uint32_t i = 0; i < chain; ++i) {
+    // the last step writes out_dev; earlier steps alternate backwards from there
+    void *dst = ((chain - 1 - i) % 2 == 0) ? out_dev : scratch_dev;
+    const qh_status st = contract == QH_CONTRACT_NONE
+                             ? qh_qmm_run(prep, m, src, dst, stream)
+                             : qh_qmm_run_contract(prep, m, src, dst, contract, divisor, stream);
+    if (st != QH_STATUS_OK) return st;
+    src = dst;
+  }
+  return QH_STATUS_OK;
+}
+
 qh_status qh_qmm_query(const qh_qmm_prepared *prep, qh_qmm_info *info) {
   if (prep == nullptr || info == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_query: NULL argument");
   const QmmShape &sh = prep->shape;

@@ -197,6 +197,24 @@ class QuantMatmul:
         _lib.check(st, "qh_qmm_run_contract")
         return out
 
+    def chain(self, act: torch.Tensor, chain: int, contract=None, divisor: int = 1,
+              out: Optional[torch.Tensor] = None, scratch: Optional[torch.Tensor] = None,
+              stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """``chain`` identical matmuls, each output the next activation (the reference's CHAIN
+        graphs), with the float requantisation (``contract=None``) or an integer contract."""
+        m = self._check_act(act)
+        cid = _lib.QH_CONTRACT_NONE if contract is None else (CONTRACTS[contract] if isinstance(contract, str)
+                                                               else int(contract))
+        if out is None:
+            out = torch.empty((m, self.n), dtype=self.out_dtype, device=act.device)
+        if scratch is None and chain > 1:
+            scratch = torch.empty_like(out)
+        st = _lib.lib().qh_qmm_run_chain(self._h, m, int(chain), act.data_ptr(), out.data_ptr(),
+                                         scratch.data_ptr() if scratch is not None else None, cid, int(divisor),
+                                         _stream_ptr(stream))
+        _lib.check(st, "qh_qmm_run_chain")
+        return out
+
     def close(self) -> None:
         if getattr(self, "_h", None) and self._h.value:
             _lib.lib().qh_qmm_release(self._h)
