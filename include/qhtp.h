@@ -174,6 +174,15 @@ qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const voi
 qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t chain, const void *act_dev,
                            void *out_dev, void *scratch_dev, uint32_t contract, uint32_t divisor, void *stream);
 
+/* qh_qmm_run_chain that allocates nothing and takes no scratch operand.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The intermediate results
+ * live in a static per-device array of 8 MiB: M x N output elements must fit in it (else
+ * QH_STATUS_SHAPE_UNSUPPORTED).  All calls on one device share that array, so calls that overlap
+ * on one device (other streams or threads) race; serialise them.  chain <= 1 uses no scratch. */
+qh_status qh_qmm_run_chain_noalloc(const qh_qmm_prepared *prep, uint32_t m, uint32_t chain, const void *act_dev,
+                                   void *out_dev, uint32_t contract, uint32_t divisor, void *stream);
+
 typedef struct qh_qmm_info {
   uint32_t k, n, act_bits, out_bits, weight_format, lpbq_block;
   uint64_t device_bytes;      /* device memory held by the prepared state */

@@ -67,6 +67,7 @@ EXPORTED = (
     "qh_qmm_accumulate",
     "qh_qmm_run_contract",
     "qh_qmm_run_chain",
+    "qh_qmm_run_chain_noalloc",
     "qh_qmm_query",
     "qh_qmm_release",
     "qh_weight_unpack",
@@ -151,6 +152,8 @@ def _declare(L: C.CDLL) -> None:
     L.qh_qmm_run_contract.restype = st
     L.qh_qmm_run_chain.argtypes = [vp, u32, u32, vp, vp, vp, u32, u32, vp]
     L.qh_qmm_run_chain.restype = st
+    L.qh_qmm_run_chain_noalloc.argtypes = [vp, u32, u32, vp, vp, u32, u32, vp]
+    L.qh_qmm_run_chain_noalloc.restype = st
     L.qh_qmm_query.argtypes = [vp, C.POINTER(QmmInfo)]
     L.qh_qmm_query.restype = st
     L.qh_qmm_release.argtypes = [vp]
