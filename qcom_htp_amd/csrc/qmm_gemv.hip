@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kGemvThreads = 256;
 constexpr int kGemvWaves = kGemvThreads / 64;
-constexpr int kGemvMaxDynLds = 148 * 1024;  // activation planes + k-group sums
+constexpr int kGemvMaxDynLds = 140 * 1024;  // activation planes + k-group sums (+ <= 17 KB static)
 constexpr int kU = kGemvKU;                  // k-groups per lane per batch (loads in flight)
 
 struct GemvArgs {
@@ -46,7 +46,7 @@ struct GemvArgs {
   const uint8_t *w;      // GEMV stream
   const uint8_t *lpbq;   // block scales, gemv_scale_index layout
   const double *alpha, *beta, *margin, *absb, *bias_deq, *mr1;
-  const int64_t *corr, *mant, *colsum;
+  const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
   int M, N, K, KG, nbatch, sub_shift;
   int act_zp, out_zp, out_qmax, out16;
@@ -67,6 +67,43 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // byte of the product and the sum below 256 (no carries between bytes); f = 0 gives zero weights.
 __device__ __forceinline__ uint32_t w4_to_i8(uint32_t u4, uint32_t f) {
   return (u4 * f + (128u - 8u * f) * 0x01010101u) ^ 0x80808080u;
+}
+
+// 16-bit activations, int4 codes: the float32 rounding residue r = fl32(w s32) / 2^E - w M of a
+// weight w = (u - 8) f depends only on the code u and the block scale f (s32 = M 2^E).  A table
+// per (column, f) holds R(j f) for j = 0..7 (bytes 0-7, codes u >= 8: index u - 8) and
+// R((u - 8) f) for u = 0..7 (bytes 8-15, codes u < 8: index u); four codes are looked up with
+// two byte permutes and a per-byte select on the code's bit 3.
+__device__ __forceinline__ uint32_t resid4(uint32_t nb, const uint4 &tab) {
+  const uint32_t sel = nb & 0x07070707u;
+  const uint32_t pos = perm(tab.y, tab.x, sel);
+  const uint32_t neg = perm(tab.w, tab.z, sel);
+  // 0xFF in the bytes whose code has bit 3 set: with y = nb << 4 that bit is each byte's sign
+  // bit, and permute selectors 8..11 replicate the sign bits of bytes 1 and 3 of either source
+  // (bytes of y << 8 and of y), in the byte order 0, 1, 2, 3
+  const uint32_t y = nb << 4;
+  const uint32_t m = perm(y, y << 8, 0x0B090A08u);
+  return (pos & m) | (neg & ~m);
+}
+
+// The residue table of (column n, block scale f): R(x) = fl32(x) - x for x = w M, computed as
+// the float32 conversion of the exact integer product (|x| < 2^31: |w| <= 112, M < 2^24), which
+// rounds like the float32 product w * s32 of the oracle.
+__device__ __forceinline__ uint4 resid_table(int Mn, int f) {
+  uint32_t b[16];
+  const int F = f * Mn;
+  b[0] = 0u;
+  b[8] = 0u;  // code 0 (q = -8) never occurs
+#pragma unroll
+  for (int j = 1; j < 8; ++j) {
+    const int x = j * F;
+    const int r = static_cast<int>(static_cast<float>(x)) - x;  // |r| <= 64
+    b[j] = static_cast<uint32_t>(r) & 0xFFu;
+    b[16 - j] = static_cast<uint32_t>(-r) & 0xFFu;  // R(-j f) = -R(j f), code u = 8 - j
+  }
+  return make_uint4(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24),
+                    b[8] | (b[9] << 8) | (b[10] << 16) | (b[11] << 24),
+                    b[12] | (b[13] << 8) | (b[14] << 16) | (b[15] << 24));
 }
 
 __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
@@ -276,16 +313,21 @@ __device__ __forceinline__ void store_unit(const GemvArgs &g, int u, ActUnit<A16
       asum[u] = static_cast<int16_t>(sh);
       asum[M * KG + u] = static_cast<int16_t>(sl);
     }
-    atomicAdd(&r1[m], rs);
+    if (FMT != kTileI4) atomicAdd(&r1[m], rs);
   }
 }
 
 template <bool A16, int FMT, bool LPBQ, int MM>
 __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kernel(const GemvArgs g) {
+  // 16-bit activations with int4 codes also form sum_k hi'_k r_k (the residue products of the
+  // high activation byte) exactly, from the residue tables of the group's 16 columns
+  constexpr bool HR = A16 && FMT == kTileI4;
   extern __shared__ uint4 smem[];
   uint8_t *const lds = reinterpret_cast<uint8_t *>(smem);
   __shared__ int red[kGemvWaves][MM][16];
   __shared__ int red2[A16 ? kGemvWaves : 1][A16 ? MM : 1][16];
+  __shared__ int red3[HR ? kGemvWaves : 1][HR ? MM : 1][16];
+  __shared__ uint4 rtab[HR ? 16 * 16 : 1];  // [column][block scale f]
   __shared__ uint32_t r1[16];
   __shared__ uint16_t fix_list[MM * 16];
   __shared__ int fix_cnt;
@@ -321,7 +363,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   // group), requested together with the group's first batch of weights.
   struct Epi {
     double alpha, beta, margin, absb, mr1;
-    int64_t corr, mant;
+    int64_t corr, mant, csr;
   } ep{};
   const bool owns_out = t < MM * 16 && (t >> 4) < M;
   auto load_epi = [&](int grp) {  // every thread loads (its column exists), only owners use it
@@ -334,6 +376,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
       ep.corr = g.colsum[n];
       ep.mr1 = g.mr1[n];
       ep.mant = g.mant[n];
+      if (HR) ep.csr = g.colsum_r[n];
     } else {
       ep.corr = g.corr[n];
     }
@@ -370,13 +413,19 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   // row from LDS once per weight word and is LDS bound there)
   constexpr bool kMfma = MM == 16;
   for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
-    int acc[kMfma ? 1 : MM], acc2[A16 && !kMfma ? MM : 1];
+    if constexpr (HR) {
+      // residue tables of this group's 16 columns, one (column, f) per thread
+      rtab[t] = resid_table(static_cast<int>(g.mant[grp * 16 + (t >> 4)]), t & 15);
+      lds_barrier();
+    }
+    int acc[kMfma ? 1 : MM], acc2[A16 && !kMfma ? MM : 1], acc3[HR && !kMfma ? MM : 1];
 #pragma unroll
     for (int m = 0; m < (kMfma ? 1 : MM); ++m) {
       acc[m] = 0;
       if (A16 && !kMfma) acc2[m] = 0;
+      if (HR && !kMfma) acc3[m] = 0;
     }
-    v4i macc = {0, 0, 0, 0}, macc2 = {0, 0, 0, 0};
+    v4i macc = {0, 0, 0, 0}, macc2 = {0, 0, 0, 0}, macc3 = {0, 0, 0, 0};
     for (int i0 = 0; i0 < iters; i0 += kU) {
       if (i0 > 0) issue(grp, i0);
       if constexpr (kMfma) {
@@ -391,9 +440,17 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
           const bool valid = kg_raw < KG;
           const int kg = valid ? kg_raw : KG - 1;
           uint32_t b[8];  // B operand dwords of products j = 0..3 (two each)
+          uint32_t rr[HR ? 8 : 1];  // residues of the same 32 weights
           if (FMT == kTileI4) {
             const uint32_t f = valid ? (LPBQ ? ((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu : 1u) : 0u;
             const uint4 v = wv[i][0];
+            if constexpr (HR) {
+              const uint4 tab = rtab[col * 16 + f];
+              rr[0] = resid4(v.x & 0x0F0F0F0Fu, tab); rr[1] = resid4(v.y & 0x0F0F0F0Fu, tab);
+              rr[2] = resid4(v.z & 0x0F0F0F0Fu, tab); rr[3] = resid4(v.w & 0x0F0F0F0Fu, tab);
+              rr[4] = resid4((v.x >> 4) & 0x0F0F0F0Fu, tab); rr[5] = resid4((v.y >> 4) & 0x0F0F0F0Fu, tab);
+              rr[6] = resid4((v.z >> 4) & 0x0F0F0F0Fu, tab); rr[7] = resid4((v.w >> 4) & 0x0F0F0F0Fu, tab);
+            }
             // byte j of the 16: k = j (low nibble), k = j + 16 (high nibble)
             b[0] = w4_to_i8(v.x & 0x0F0F0F0Fu, f); b[1] = w4_to_i8(v.y & 0x0F0F0F0Fu, f);
             b[2] = w4_to_i8(v.z & 0x0F0F0F0Fu, f); b[3] = w4_to_i8(v.w & 0x0F0F0F0Fu, f);
@@ -410,6 +467,8 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
           for (int j = 0; j < 4; ++j) {
             const uint2 a = ap[j];
             macc = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(b[2 * j], b[2 * j + 1]), macc, 0, 0, 0);
+            if constexpr (HR)
+              macc3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(rr[2 * j], rr[2 * j + 1]), macc3, 0, 0, 0);
           }
           if (A16) {
             const uint2 *lp = reinterpret_cast<const uint2 *>(lds + static_cast<size_t>(M + mrow) * K + kg * 32);
@@ -441,6 +500,12 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         }
         const int a8 = valid ? 8 : 0;  // the -8 offset of the unsigned nibble codes
         const int f = LPBQ ? static_cast<int>(((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu) : 1;
+        uint32_t rr[HR ? 8 : 1];  // residues of the 32 weights (zero codes in slots past K: r = 0)
+        if constexpr (HR) {
+          const uint4 tab = rtab[col * 16 + (valid ? f : 0)];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) rr[j] = resid4(w[j], tab);
+        }
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
           if (MM > 1 && m >= M) continue;
@@ -460,6 +525,12 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
             if (FMT == kTileI4) e -= a8 * asum[(M + m) * KG + kg];
             acc2[m] += LPBQ ? e * f : e;
           }
+          if constexpr (HR) {
+            int h = sdot4(a0.x, rr[0], acc3[m]);
+            h = sdot4(a0.y, rr[1], h); h = sdot4(a0.z, rr[2], h); h = sdot4(a0.w, rr[3], h);
+            h = sdot4(a1.x, rr[4], h); h = sdot4(a1.y, rr[5], h); h = sdot4(a1.z, rr[6], h); h = sdot4(a1.w, rr[7], h);
+            acc3[m] = h;
+          }
         }
       }
     }
@@ -472,6 +543,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
       for (int q = 0; q < 4; ++q) {
         red[wave][4 * sub + q][col] = macc[q];
         if (A16) red2[wave][4 * sub + q][col] = macc2[q];
+        if (HR) red3[wave][4 * sub + q][col] = macc3[q];
       }
     }
 #pragma unroll
@@ -484,25 +556,41 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         acc2[m] += __shfl_xor(acc2[m], 32, 64);
         if (sub == 0) red2[wave][m][col] = acc2[m];
       }
+      if (HR) {
+        acc3[m] += __shfl_xor(acc3[m], 16, 64);
+        acc3[m] += __shfl_xor(acc3[m], 32, 64);
+        if (sub == 0) red3[wave][m][col] = acc3[m];
+      }
     }
     lds_barrier();
     // requantise: thread t owns output (row t / 16, column t % 16) of the group
     const int om = t >> 4, n = grp * 16 + (t & 15);
     bool amb = false;
     if (owns_out) {
-      int S1 = 0, S2 = 0;
+      int S1 = 0, S2 = 0, S3 = 0;
 #pragma unroll
       for (int w = 0; w < kGemvWaves; ++w) {
         S1 += red[w][om][t & 15];
         if (A16) S2 += red2[w][om][t & 15];
+        if (HR) S3 += red3[w][om][t & 15];
       }
-      const double alpha = A16 ? ep.alpha * static_cast<double>(ep.mant) : ep.alpha;
       const double beta = ep.beta, margin = ep.margin, absb = ep.absb, mr1 = ep.mr1;
       const int64_t corr = A16 ? ep.corr * static_cast<int64_t>(128 + 32768 - g.act_zp) : ep.corr;
       const int64_t S = A16 ? 256 * static_cast<int64_t>(S1) + S2 + corr : static_cast<int64_t>(S1) + corr;
-      const double tv = fma(static_cast<double>(S), alpha, beta);
+      double tv, slack;
+      if constexpr (HR) {
+        // D = sum_k (a - zp) (w M + r) but for sum_k lo'_k r_k, bounded by mr1:
+        //   M S + 256 sum hi' r + (32896 - zp) sum r
+        const int64_t D = S * ep.mant + 256 * static_cast<int64_t>(S3) +
+                          static_cast<int64_t>(128 + 32768 - g.act_zp) * ep.csr;
+        tv = fma(static_cast<double>(D), ep.alpha, beta);
+        slack = margin + mr1 + 0x1p-48 * (fabs(tv) + absb);
+      } else {
+        const double alpha = A16 ? ep.alpha * static_cast<double>(ep.mant) : ep.alpha;
+        tv = fma(static_cast<double>(S), alpha, beta);
+        slack = margin + (A16 ? mr1 * static_cast<double>(r1[om]) : 0.0) + 0x1p-48 * (fabs(tv) + absb);
+      }
       const double fl = floor(tv);
-      const double slack = margin + (A16 ? mr1 * static_cast<double>(r1[om]) : 0.0) + 0x1p-48 * (fabs(tv) + absb);
       const bool near_tie = fabs((tv - fl) - 0.5) <= slack;
       const double lo = fmin(fmax(fl, 0.0), static_cast<double>(g.out_qmax));
       const double hi = fmin(fmax(fl + 1.0, 0.0), static_cast<double>(g.out_qmax));
@@ -654,6 +742,7 @@ qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void
   g.corr = D.corr;
   g.mant = D.mant;
   g.colsum = D.colsum;
+  g.colsum_r = D.colsum_r;
   g.s32 = D.s32;
   g.M = m;
   g.N = sh.N;

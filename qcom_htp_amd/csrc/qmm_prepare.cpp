@@ -455,7 +455,11 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
       const int64_t sum_wp = mant[n] * colsum_q[n] + colsum_r[n];
       corr[n] = static_cast<int64_t>(128 + 32768 - d->act_zp) * sum_wp;
       margin[n] = inv_sO * sA * two_e * noise * kSafety;
-      mr1[n] = inv_sO * sA * two_e * rmax[n] * kSafety;  // GEMV: residue term bound per unit R1
+      // GEMV residue term.  int4 codes: the GEMV forms sum_k hi'_k r_k exactly (hi' the high
+      // activation byte minus 128), so only sum_k lo'_k r_k (|lo'| <= 128) is bounded, by a
+      // constant.  int8 codes: the whole term is bounded, per unit of R1 = sum_k |a_k - zp|.
+      mr1[n] = sh.gemv_fmt == kTileI4 ? inv_sO * sA * two_e * 128.0 * r1[n] * kSafety
+                                      : inv_sO * sA * two_e * rmax[n] * kSafety;
     }
     beta[n] = bdeq[n] / sO + d->out_zp;
     {

@@ -272,3 +272,22 @@ def test_w16a16_split_identity_and_brute_force():
     for i in range(4):
         for j in range(5):
             assert acc[i, j] == sum((int(x[i, k]) - 32768) * int(q16[j, k]) for k in range(24))
+
+
+def test_residue_from_integer_product_matches_float32_product():
+    """fl32(w * s32) / 2^E - w * M equals float32(w * M) - w * M for s32 = M 2^E (the GEMV's
+    residue tables rely on it): the float32 multiply and the int -> float32 conversion both
+    round the same exact product to 24 bits, to nearest even."""
+    rng = np.random.default_rng(77)
+    s = rng.uniform(1e-4, 1e2, size=4000).astype(np.float32)
+    s = np.concatenate([s, (s.view(np.uint32) | np.uint32(1)).view(np.float32)])  # odd mantissas
+    fr, e = np.frexp(s.astype(np.float64))
+    M = np.ldexp(fr, 24).astype(np.int64)
+    E = e - 24
+    w = np.arange(-127, 128, dtype=np.int64)
+    prod = (w[None, :].astype(np.float32) * s[:, None]).astype(np.float64)
+    r_oracle = np.ldexp(prod, -E[:, None]).astype(np.int64) - w[None, :] * M[:, None]
+    x = w[None, :] * M[:, None]
+    r_int = x.astype(np.float32).astype(np.int64) - x
+    np.testing.assert_array_equal(r_int, r_oracle)
+    assert np.abs(r_oracle).max() <= 64

@@ -169,7 +169,7 @@ def test_gemv_near_tie_decode_rows_bit_exact(gpu, fam, k, rows):
     c = near_tie_case(fam, 16, k, 96, 7, tie_rows=[0, 2, 9], zero_rows=[3, 12], rail_rows=[1, 15])
     want = oq.expected_output_case(c)[:rows]
     print(f"[qmm] {fam} near-tie gemv rows={rows} k={k}", flush=True)
-    if c.family.act_bits == 16 and 2 * rows * k > 148 * 1024:
+    if c.family.act_bits == 16 and 2 * rows * k > 140 * 1024:
         # the forced GEMV path stages every row in LDS: 16-bit rows this long do not fit and the
         # entry point says so (the automatic path takes the GEMM for them)
         from qcom_htp_amd import _lib
