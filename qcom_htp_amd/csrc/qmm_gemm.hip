@@ -53,6 +53,7 @@ struct GemmArgs {
   const uint8_t *tiles;
   const double *alpha, *beta, *margin, *absb, *bias_deq;
   const double *alpha_e, *margin_exact;
+  const double *margin_lo;  // 16-bit acts: bound of the low-byte residue sum (output LSB)
   const int32_t *scale_exp;
   const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
@@ -407,20 +408,30 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
       read_step<A16>(c, na, nb, kk - 2, p.raw[kk & 1]);
     // operands of step sigma + 1
     convert_step<A16>(p.raw[(kk + 1) & 1], p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
-    // MFMAs of step sigma
+    // MFMAs of step sigma.  16-bit acts: fragments mt = 2 i (high bytes) and 2 i + 1 (low
+    // bytes) of row block i; columns nt = 0 (weight codes) and 1 (rounding residues).  The low
+    // bytes' residue products are left out: their sum is bounded (|lo'| <= 128) and completed
+    // only for listed outputs.
     static_for<4>([&](auto mt) {
       static_for<kNT>([&](auto nt) {
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(p.af[kk & 1][mt], p.bf[kk & 1][nt], acc[mt][nt], 0, 0, 0);
+        if constexpr (!(A16 && (decltype(mt)::value & 1) && decltype(nt)::value == 1))
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(p.af[kk & 1][mt], p.bf[kk & 1][nt], acc[mt][nt], 0, 0, 0);
       });
     });
     // issue order: the fragment reads early, then one MFMA and a few conversion instructions
     // at a time
-    constexpr int kValu = A16 ? 3 : 2;  // conversion work per MFMA
-    static_for<4 * kNT>([&](auto i) {
+    constexpr int kMfmas = A16 ? 6 : 4 * kNT;
+    constexpr int kValu = A16 ? 4 : 2;  // conversion work per MFMA
+    static_for<kMfmas>([&](auto i) {
       constexpr int ii = decltype(i)::value;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if constexpr (ii < 4 + kNT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if constexpr (kk == 2 && ii < C::kLoads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if constexpr (kk == 2) {
+        // the stage's tile loads, spread over the step's MFMAs
+        constexpr int per = (C::kLoads + kMfmas - 1) / kMfmas;
+        constexpr int n = C::kLoads - ii * per < per ? (C::kLoads - ii * per > 0 ? C::kLoads - ii * per : 0) : per;
+        if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);
+      }
       __builtin_amdgcn_sched_group_barrier(0x002, kValu + (kk == 2 ? 4 : 0), 0);
     });
   });
@@ -479,7 +490,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   if (MODE == 0) {
     cv[0] = g.alpha[cn];
     cv[1] = g.beta[cn];
-    cv[2] = g.margin[cn];
+    cv[2] = g.margin[cn] + (A16 ? g.margin_lo[cn] : 0.0);
     cv[3] = g.absb[cn];
     ccorr = g.corr[cn];
     if (A16) cmant = g.mant[cn];
@@ -654,7 +665,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
           auto t_of = [&](auto jj) {
             constexpr int j = 4 * decltype(jg)::value + decltype(jj)::value;
             const double X = fma(static_cast<double>(acc[2 * mt][2 * c][j]), 256.0, static_cast<double>(acc[2 * mt + 1][2 * c][j]));
-            const double Y = fma(static_cast<double>(acc[2 * mt][2 * c + 1][j]), 256.0, static_cast<double>(acc[2 * mt + 1][2 * c + 1][j]));
+            const double Y = 256.0 * static_cast<double>(acc[2 * mt][2 * c + 1][j]);  // high-byte residue sum
             return fma(Y, alpha, fma(X, alpha_m, beta));
           };
           int o[4];
@@ -676,7 +687,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
                 if (slot < kFixCap) {
                   fix_list[slot] = (static_cast<uint32_t>(r) << 16) | static_cast<uint32_t>(cl);
                   fix_val[2 * slot] = 256 * static_cast<int64_t>(acc[2 * mt][2 * c][j]) + acc[2 * mt + 1][2 * c][j];
-                  fix_val[2 * slot + 1] = 256 * static_cast<int64_t>(acc[2 * mt][2 * c + 1][j]) + acc[2 * mt + 1][2 * c + 1][j];
+                  fix_val[2 * slot + 1] = 256 * static_cast<int64_t>(acc[2 * mt][2 * c + 1][j]);
                 } else {
                   keep |= 1u << decltype(jjc)::value;  // beyond the list: a later pass
                 }
@@ -753,6 +764,32 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
              (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32))) << 32);
         S2 = static_cast<long long>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(y)))) |
              (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(y >> 32))) << 32);
+        // + sum_k lo'_k r_k: low activation bytes (a & 255) - 128 times the residue column of the
+        // weight tiles, 16 k per lane and chunk; chunks past K count as zero
+        const int cr = (n / 32) * 64 + 32 + (n % 32);
+        const uint16_t *const arow = reinterpret_cast<const uint16_t *>(act) + static_cast<size_t>(m) * K;
+        int s2l = 0;  // |.| <= 128 * 64 * K < 2^31
+        for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
+          uint4 rv[P], av[P][2];
+#pragma unroll
+          for (int pp = 0; pp < P; ++pp) {
+            const int kc = kc0 + lane + 64 * pp;
+            const int k = (kc < KC ? kc : 0) * 16;
+            rv[pp] = load_w16_raw(g, cr, k);
+            av[pp][0] = *reinterpret_cast<const uint4 *>(arow + k);
+            av[pp][1] = *reinterpret_cast<const uint4 *>(arow + k + 8);
+          }
+#pragma unroll
+          for (int pp = 0; pp < P; ++pp) {
+            const uint32_t keep = kc0 + lane + 64 * pp < KC ? 0xFFFFFFFFu : 0u;
+            const uint4 a0 = av[pp][0], a1 = av[pp][1];
+            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a0.y, a0.x, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].x & keep), s2l, false);
+            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a0.w, a0.z, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].y & keep), s2l, false);
+            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a1.y, a1.x, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].z & keep), s2l, false);
+            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a1.w, a1.z, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].w & keep), s2l, false);
+          }
+        }
+        S2 += wave_sum(s2l);
       }
       // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
       const unsigned long long M64 = static_cast<unsigned long long>(mant_n);
@@ -936,6 +973,7 @@ qh_status dispatch(const qh_qmm_prepared *p, int m, const void *act, void *out, 
   g.alpha_e = D.alpha_e;
   g.scale_exp = D.scale_exp;
   g.margin_exact = D.margin_exact;
+  g.margin_lo = D.margin_lo;
   g.s32 = D.s32;
   g.resid = D.resid;
   g.M = m;

@@ -45,7 +45,7 @@ struct GemvArgs {
   void *out;
   const uint8_t *w;      // GEMV stream
   const uint8_t *lpbq;   // block scales, gemv_scale_index layout
-  const double *alpha, *beta, *margin, *absb, *bias_deq, *mr1;
+  const double *alpha, *beta, *margin, *absb, *bias_deq, *mr1, *mlo;
   const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
   int M, N, K, KG, nbatch, sub_shift;
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     ep.absb = g.absb[n];
     if (A16) {
       ep.corr = g.colsum[n];
-      ep.mr1 = g.mr1[n];
+      ep.mr1 = HR ? g.mlo[n] : g.mr1[n];
       ep.mant = g.mant[n];
       if (HR) ep.csr = g.colsum_r[n];
     } else {
@@ -739,6 +739,7 @@ qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void
   g.absb = D.absb;
   g.bias_deq = D.bias_deq;
   g.mr1 = D.gemv_margin_r1;
+  g.mlo = D.margin_lo;
   g.corr = D.corr;
   g.mant = D.mant;
   g.colsum = D.colsum;

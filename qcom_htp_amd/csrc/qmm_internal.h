@@ -79,8 +79,9 @@ struct QmmDevice {
   double *alpha_e;  // sA * 2^E / sO: output LSB per unit of the exact integer dot product in 2^E units
   int32_t *scale_exp; // E of s32 = M * 2^E
   double *margin_exact; // 8-bit acts: float64 noise bound of the oracle's dot product, output LSB
-  double *gemv_margin_r1; // 16-bit acts GEMV: int4 codes: bound of the low-byte residue term (output
-                          // LSB); int8 codes: per-channel coefficient of R1[m] = sum |a - zp| in the margin
+  double *gemv_margin_r1; // 16-bit acts, int8-code GEMV: coefficient of R1[m] = sum |a - zp| in the margin
+  double *margin_lo;      // 16-bit acts: bound of sum_k lo'_k r_k in output LSB (the GEMM and the int4-code
+                          // GEMV form the high-byte residue sum exactly)
   int8_t *resid;    // 8-bit acts: rounding residues r[n][k] (fl32(w s32) = 2^E (w M + r)), [N][K],
                     // read by the GEMM's exact fixup (|r| <= 64)
   int32_t *bias_q;  // [Np] the descriptor's int32 bias (integer contracts)

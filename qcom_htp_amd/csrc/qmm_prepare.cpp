@@ -429,7 +429,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   const double sA = d->act_scale, sO = d->out_scale, inv_sO = 1.0 / sO;
   const double amax = static_cast<double>(std::max(d->act_zp, act_qmax - d->act_zp));
   const int Np = sh.Np;
-  std::vector<double> alpha(Np, 0.0), beta(Np, 0.0), margin(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0), mr1(Np, 0.0);
+  std::vector<double> alpha(Np, 0.0), beta(Np, 0.0), margin(Np, 0.0), absb(Np, 1.0), bdeq(Np, 0.0), mr1(Np, 0.0),
+      mlo(Np, 0.0);
   std::vector<int64_t> corr(Np, 0), mantv(Np, 0), csum(Np, 0), csum_r(Np, 0);
   std::vector<double> alpha_e(Np, 0.0);
   std::vector<double> margin_exact(Np, 0.0);
@@ -455,11 +456,12 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
       const int64_t sum_wp = mant[n] * colsum_q[n] + colsum_r[n];
       corr[n] = static_cast<int64_t>(128 + 32768 - d->act_zp) * sum_wp;
       margin[n] = inv_sO * sA * two_e * noise * kSafety;
-      // GEMV residue term.  int4 codes: the GEMV forms sum_k hi'_k r_k exactly (hi' the high
-      // activation byte minus 128), so only sum_k lo'_k r_k (|lo'| <= 128) is bounded, by a
-      // constant.  int8 codes: the whole term is bounded, per unit of R1 = sum_k |a_k - zp|.
-      mr1[n] = sh.gemv_fmt == kTileI4 ? inv_sO * sA * two_e * 128.0 * r1[n] * kSafety
-                                      : inv_sO * sA * two_e * rmax[n] * kSafety;
+      // Residue term sum_k (a_k - zp) r_k.  The GEMM and the int4 GEMV form its high-byte part
+      // sum_k hi'_k r_k exactly (hi' the high activation byte minus 128); the low-byte part
+      // sum_k lo'_k r_k (|lo'| <= 128) is bounded by margin_lo.  The int8 GEMV bounds the whole
+      // term, per unit of R1 = sum_k |a_k - zp| (mr1).
+      mr1[n] = inv_sO * sA * two_e * rmax[n] * kSafety;
+      mlo[n] = inv_sO * sA * two_e * 128.0 * r1[n] * kSafety;
     }
     beta[n] = bdeq[n] / sO + d->out_zp;
     {
@@ -510,6 +512,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.scale_exp, scale_exp);
   if (st == QH_STATUS_OK) st = al.upload(&D.margin_exact, margin_exact);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_margin_r1, mr1);
+  if (st == QH_STATUS_OK && a16) st = al.upload(&D.margin_lo, mlo);
   if (st == QH_STATUS_OK && !a16) st = al.upload(&D.resid, resid);
   if (st == QH_STATUS_OK) st = al.upload(&D.bias_q, biasv);
   if (st == QH_STATUS_OK) st = al.upload(&D.corr_int, corr_int);
