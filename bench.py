@@ -208,6 +208,49 @@ def gdn_chunk_workload(B: int, T: int, H: int, C: int, steps: int, warmup: int):
             "oc_vs_fp64_worst_of_8_items": worst}
 
 
+def gdn_prefill_workload(B: int, T: int, H: int, steps: int, warmup: int, precision: int):
+    """The chunked prefill at chunk 64: stage A (W, U; float32 for FP32, bf16 for BF16) then the
+    chunk recurrence (stage B, o bf16 and the final state), timed as one step and per kernel."""
+    import torch
+
+    from qcom_htp_amd.gdn import FP32, gdn_chunk_state, gdn_chunk_uw, gdn_prefill
+
+    D = 128
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    q, k, v = (torch.randn((B, T, H, D), generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
+    beta = torch.sigmoid(torch.randn((B, T, H), generator=gen, device=dev))
+    gc = torch.nn.functional.logsigmoid(torch.randn((B, T, H), generator=gen, device=dev) + 3.0)
+    wu_dtype = torch.float32 if precision == FP32 else torch.bfloat16
+    wall, ev = time_kernel(lambda i: gdn_prefill(q, k, v, gc, beta, precision=precision), steps, warmup)
+    w, u = gdn_chunk_uw(k, v, gc, beta, 64, decay_w=True, out_dtype=wu_dtype)
+    wall_b, ev_b = time_kernel(lambda i: gdn_chunk_state(q, k, gc, w, u, precision=precision), steps, warmup)
+    # stage B bytes: q, k (bf16), W, U, o (bf16), gc, the final state
+    wu_b = 4 if precision == FP32 else 2
+    nbytes_b = B * T * H * (D * (2 + 2 + 2 * wu_b + 2) + 4) + B * H * D * D * 4
+    # stage B flops per chunk-head: q k^T, W S, q S, P v_new, k^T v_new
+    flops_b = B * H * (T // 64) * 2.0 * (64 * 64 * D * 2 + 3 * 64 * D * D)
+    # after the timed region: two whole sequences against the float64 oracle
+    import numpy as np
+
+    from oracle import gdn as og  # the checker
+
+    o, S = gdn_prefill(q, k, v, gc, beta, precision=precision)
+    worst = 0.0
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        seq = lambda x: x[b, :, h].double().cpu().numpy()[None]
+        o_ref, S_ref = og.gdn_prefill_torch(seq(q), seq(k), seq(v), seq(gc), seq(beta), 64)
+        worst = max(worst, og.oc(o[b, :, h].double().cpu().numpy(), o_ref.numpy()[0]),
+                    og.oc(S[b, h].double().cpu().numpy(), S_ref.numpy()[0]))
+    if not worst <= og.GATE_BF16:
+        raise RuntimeError(f"GDN prefill: oc {worst:.3e} > {og.GATE_BF16}")
+    return {"B": B, "T": T, "H": H, "chunk": 64, "precision": "fp32" if precision == FP32 else "bf16", "ms": ev,
+            "wall_ms": wall, "tokens_per_s": B * T / (ev * 1e-3), "stage_b_ms": ev_b, "stage_b_wall_ms": wall_b,
+            "stage_b_bytes": nbytes_b, "stage_b_gbs": nbytes_b / (ev_b * 1e-3) / 1e9,
+            "stage_b_tflops_alg": flops_b / (ev_b * 1e-3) / 1e12, "oc_vs_fp64_worst_of_2_sequences": worst}
+
+
 def cpu_baseline(case, gdn_A):
     """The oracle (numpy/LAPACK/torch restatement of the reference's CPU path) on the host cores
     of this job: one warm-up, then the median of 5 runs per shape (3 for the slowest)."""
@@ -373,6 +416,9 @@ def main() -> int:
             jobs.append((f"gdn_c256_h32_{'fp32' if prec == 0 else 'bf16'}", lambda prec=prec: gdn_workload(32, 256, 50, 5, prec)))
         for C in (64, 256):
             jobs.append((f"gdn_chunk_uw_c{C}", lambda C=C: gdn_chunk_workload(8, 4096, 32, C, 10, 2)))
+        for prec in (0, 1):
+            jobs.append((f"gdn_prefill_c64_{'fp32' if prec == 0 else 'bf16'}",
+                         lambda prec=prec: gdn_prefill_workload(8, 4096, 32, 10, 2, prec)))
         jobs.append(("lpbq_expand_4096x14336", lambda: lpbq_expand_workload(4096, 14336, 20, 3)))
         for key, job in jobs:
             if args.only and not re.search(args.only, key):

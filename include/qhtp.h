@@ -280,7 +280,8 @@ qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t head
  * relative Frobenius against float64).  Buffers must be 16-byte aligned. */
 enum {
   QH_GDN_W_DECAY = 1u, /* W = T (beta * K^ * e^g) (the reference kernel's form)           */
-  QH_GDN_OUT_F32 = 2u, /* W and U as float32 instead of bf16                             */
+  QH_GDN_OUT_F32 = 2u, /* W and U (qh_gdn_chunk_state: o) as float32 instead of bf16      */
+  QH_GDN_WU_F32 = 4u,  /* qh_gdn_chunk_state: w_dev and u_dev hold float32, not bf16      */
 };
 qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const float *g_dev, const float *beta_dev,
                           void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
@@ -295,6 +296,26 @@ qh_status qh_gdn_chunk_uw_ex(const uint16_t *k_dev, const uint16_t *v_dev, const
                              void *w_dev, void *u_dev, uint32_t batch, uint32_t tokens, uint32_t heads,
                              uint32_t head_dim, uint32_t chunk, uint32_t flags, uint32_t max_workgroups,
                              void *stream);
+
+/* GDN chunk recurrence (the inter-chunk half of the gated delta rule; replaces the stage-B lines
+ * of gdn_chunk, scripts/gdn_ref_kernel.py:91-101, run over the chunk loop of gdn_kernel,
+ * :104-131).  For every batch b and head h, over the chunks of 64 tokens in order, with the
+ * state S (128 x 128, keys x values) carried from s_in_dev (NULL: zero) to s_out_dev:
+ *   q^ = l2norm(q) / sqrt(128), k^ = l2norm(k), g = cumsum of gc inside the chunk,
+ *   P = (q^ k^T) e^{g_i - g_j} (j <= i), v_new = U - W S, o = (q^ e^g) S + P v_new,
+ *   S = S e^{g_last} + (k^ e^{g_last - g})^T v_new,
+ * where W, U are qh_gdn_chunk_uw's outputs for chunk 64 with QH_GDN_W_DECAY.
+ * q_dev, k_dev: bf16 bit patterns [batch][tokens][heads][128]; g_dev (gc): float32
+ * [batch][tokens][heads]; w_dev, u_dev: [batch][tokens][heads][128] bf16 bit patterns, or float32
+ * with QH_GDN_WU_F32; o_dev: the same layout, bf16, or float32 with QH_GDN_OUT_F32;
+ * s_in_dev, s_out_dev: float32 [batch][heads][128][128] (s_out_dev must not alias s_in_dev).
+ * head_dim == 128, chunk == 64, tokens % 64 == 0 (zero-pad: zero q, k, v, beta and gc tokens
+ * leave o and S unchanged).  precision: QH_GDN_FP32 (bf16 hi/lo split products, fp32
+ * accumulation) or QH_GDN_BF16.  Buffers must be 16-byte aligned. */
+qh_status qh_gdn_chunk_state(const uint16_t *q_dev, const uint16_t *k_dev, const float *g_dev, const void *w_dev,
+                             const void *u_dev, const float *s_in_dev, float *s_out_dev, void *o_dev, uint32_t batch,
+                             uint32_t tokens, uint32_t heads, uint32_t head_dim, uint32_t chunk, uint32_t flags,
+                             uint32_t precision, void *stream);
 
 #ifdef __cplusplus
 }

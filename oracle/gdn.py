@@ -23,6 +23,17 @@ Functions and the reference lines they follow
                          intra-chunk stage (l2norm, A-build, recurrence, U, W) in torch float64,
                          batched over heads as the reference runs them
                          (scripts/gdn_ref_kernel.py:71-89); the CPU baseline times these.
+* ``chunk_state_torch`` -- the inter-chunk stage B over a whole sequence of chunks, from the
+                         stage-A outputs W (e^g form) and U: P = (q^ k^T) decay (causal),
+                         v_new = U - W S, o = (q^ e^g) S + P v_new, S <- S e^{g_last} +
+                         (k^ e^{g_last - g})^T v_new, with q^ = l2norm(q) / sqrt(D)
+                         (scripts/gdn_ref_kernel.py:66-69,91-101 and the chunk loop :104-131).
+* ``gdn_prefill_torch`` -- stage A then stage B per chunk: the reference's ``gdn_kernel``
+                         (scripts/gdn_ref_kernel.py:54-131), zero-padding T to whole chunks.
+* ``gdn_recurrent``   -- the gated delta rule token by token (decay, delta-rule write,
+                         read-out): S <- S e^{g_t}; S <- S + beta_t k^_t (v_t - S^T k^_t)^T;
+                         o_t = S^T q^_t.  An independent statement of what the chunked form
+                         computes, used to pin it.
 
 Pinning
 -------
@@ -35,6 +46,10 @@ Pinning
   A = 0; a rank-one check on two tokens).
 * ``forward_subst_torch`` and ``chunk_stage_a_torch`` are pinned against LAPACK's inverse
   (``inverse_fp64``) with ``build_A`` / ``chunk_uw``.
+* ``gdn_prefill_torch`` (and with it ``chunk_state_torch``) is pinned against
+  ``gdn_recurrent``, a token-by-token derivation that shares no code with it, at several chunk
+  sizes (the chunked result does not depend on the chunk size), with and without an incoming
+  state, and with a ragged T (zero padding must not change the result).
 """
 
 from __future__ import annotations
@@ -54,6 +69,9 @@ __all__ = [
     "chunk_uw",
     "forward_subst_torch",
     "chunk_stage_a_torch",
+    "chunk_state_torch",
+    "gdn_prefill_torch",
+    "gdn_recurrent",
     "GATE_BF16",
     "GATE_FP32",
     "SA_REF",
@@ -207,3 +225,82 @@ def chunk_stage_a_torch(k, v, gc, beta, decay_w: bool = True):
     U = T @ v_beta
     W = T @ (k_beta * torch.exp(g).unsqueeze(-1) if decay_w else k_beta)
     return U, W
+
+
+def _l2n(x):
+    import torch
+
+    return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+
+def chunk_state_torch(q, k, gc, W, U, S_in=None, C: int = 64):
+    """Stage B over whole sequences, torch float64 (scripts/gdn_ref_kernel.py:66-69,91-101).
+
+    q, k [n, T, D] (raw; l2norm and 1/sqrt(D) applied here), gc [n, T] per-token log decays,
+    W, U [n, T, D] the stage-A outputs of the same chunking (W in the T (beta k^ e^g) form),
+    S_in [n, D, D] or None.  Returns (o [n, T, D], S_out [n, D, D])."""
+    import torch
+
+    f64 = torch.float64
+    q, k, gc, W, U = (torch.as_tensor(x, dtype=f64) for x in (q, k, gc, W, U))
+    n, T, D = q.shape
+    assert T % C == 0
+    qn = _l2n(q) * (1.0 / D ** 0.5)
+    kn = _l2n(k)
+    S = torch.zeros(n, D, D, dtype=f64) if S_in is None else torch.as_tensor(S_in, dtype=f64).clone()
+    o = torch.zeros(n, T, D, dtype=f64)
+    causal = torch.tril(torch.ones(C, C, dtype=torch.bool))
+    for c0 in range(0, T, C):
+        sl = slice(c0, c0 + C)
+        g = torch.cumsum(gc[:, sl], dim=-1)
+        decay = torch.exp(torch.where(causal, g.unsqueeze(-1) - g.unsqueeze(-2), torch.zeros((), dtype=f64))) * causal
+        P = (qn[:, sl] @ kn[:, sl].transpose(-1, -2)) * decay
+        v_new = U[:, sl] - W[:, sl] @ S
+        o[:, sl] = (qn[:, sl] * torch.exp(g).unsqueeze(-1)) @ S + P @ v_new
+        g_last = g[:, -1]
+        dec = torch.exp(g_last.unsqueeze(-1) - g).unsqueeze(-1)
+        S = S * torch.exp(g_last)[:, None, None] + (kn[:, sl] * dec).transpose(-1, -2) @ v_new
+    return o, S
+
+
+def gdn_prefill_torch(q, k, v, gc, beta, C: int = 64, S_in=None):
+    """The reference's chunked prefill (scripts/gdn_ref_kernel.py:54-131) in torch float64 on
+    [n, T, D] / [n, T] inputs: zero-pad T to whole chunks, stage A per chunk
+    (``chunk_stage_a_torch``, W in the e^g form), then stage B.  Returns (o [n, T, D], S)."""
+    import torch
+
+    f64 = torch.float64
+    q, k, v, gc, beta = (torch.as_tensor(x, dtype=f64) for x in (q, k, v, gc, beta))
+    n, T, D = q.shape
+    pad = (-T) % C
+    if pad:
+        F = torch.nn.functional
+        q, k, v = (F.pad(x, (0, 0, 0, pad)) for x in (q, k, v))
+        gc, beta = F.pad(gc, (0, pad)), F.pad(beta, (0, pad))
+    Tp = T + pad
+    U, W = chunk_stage_a_torch(k.reshape(n * Tp // C, C, D), v.reshape(n * Tp // C, C, D),
+                               gc.reshape(n * Tp // C, C), beta.reshape(n * Tp // C, C), decay_w=True)
+    o, S = chunk_state_torch(q, k, gc, W.reshape(n, Tp, D), U.reshape(n, Tp, D), S_in, C)
+    return o[:, :T], S
+
+
+def gdn_recurrent(q, k, v, gc, beta, S_in=None):
+    """The gated delta rule one token at a time, torch float64 on [n, T, D] / [n, T] inputs:
+    S <- S e^{gc_t};  S <- S + beta_t k^_t (v_t - S^T k^_t)^T;  o_t = S^T q^_t, with
+    k^ = l2norm(k), q^ = l2norm(q) / sqrt(D).  Returns (o, S)."""
+    import torch
+
+    f64 = torch.float64
+    q, k, v, gc, beta = (torch.as_tensor(x, dtype=f64) for x in (q, k, v, gc, beta))
+    n, T, D = q.shape
+    qn = _l2n(q) * (1.0 / D ** 0.5)
+    kn = _l2n(k)
+    S = torch.zeros(n, D, D, dtype=f64) if S_in is None else torch.as_tensor(S_in, dtype=f64).clone()
+    o = torch.zeros(n, T, D, dtype=f64)
+    for t in range(T):
+        S = S * torch.exp(gc[:, t])[:, None, None]
+        kt = kn[:, t]
+        delta = (v[:, t] - torch.einsum("nkv,nk->nv", S, kt)) * beta[:, t, None]
+        S = S + kt[:, :, None] * delta[:, None, :]
+        o[:, t] = torch.einsum("nkv,nk->nv", S, qn[:, t])
+    return o, S

@@ -55,6 +55,7 @@ QH_GDN_BF16 = 1
 
 QH_GDN_W_DECAY = 1
 QH_GDN_OUT_F32 = 2
+QH_GDN_WU_F32 = 4
 
 # Every symbol include/qhtp.h declares (checked by the CPU test-suite).
 EXPORTED = (
@@ -76,6 +77,7 @@ EXPORTED = (
     "qh_gdn_solve_u16",
     "qh_gdn_chunk_uw",
     "qh_gdn_chunk_uw_ex",
+    "qh_gdn_chunk_state",
 )
 
 
@@ -170,6 +172,8 @@ def _declare(L: C.CDLL) -> None:
     L.qh_gdn_chunk_uw.restype = st
     L.qh_gdn_chunk_uw_ex.argtypes = [vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, vp]
     L.qh_gdn_chunk_uw_ex.restype = st
+    L.qh_gdn_chunk_state.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, u32, vp]
+    L.qh_gdn_chunk_state.restype = st
 
 
 def lib() -> C.CDLL:

@@ -36,15 +36,13 @@
 // The u16 variant applies the GdnSolve op's code contract on load / store
 // (A = (code - zpA) * sA; T_code = clip(rint(T / sT) + zpT, 0, 65535)).
 
+#include "bf16_split.h"
 #include "qmm_internal.h"
 
 namespace qh {
 namespace {
 
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+using namespace bf16s;
 
 constexpr int kRdThreads = 512;
 constexpr int kTs = 132;   // LDS row stride of the T store, words (conflict-free column reads)
@@ -60,62 +58,6 @@ struct GdnArgs {
 };
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi, lo, sel);
-}
-
-// Two floats -> packed bf16 (a in the low half), round to nearest even.
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2bf));
-}
-
-// x as one LDS word: bf16 hi in the low half, bf16(x - hi) in the high half (0 without SPLIT).
-template <bool SPLIT>
-__device__ __forceinline__ uint32_t hilo(float x) {
-  const uint32_t h = pack_bf16(x, 0.0f) & 0xFFFFu;
-  if (!SPLIT) return h;
-  return h | (pack_bf16(x - __uint_as_float(h << 16), 0.0f) << 16);
-}
-
-// 4 operand values (4 k of one MFMA row / column): the bf16 hi parts and lo parts, two per dword.
-struct Half4 {
-  uint32_t h01, h23, l01, l23;
-};
-// ... from 4 LDS words
-__device__ __forceinline__ Half4 unpack4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3) {
-  return {perm(d1, d0, 0x05040100u), perm(d3, d2, 0x05040100u), perm(d1, d0, 0x07060302u), perm(d3, d2, 0x07060302u)};
-}
-__device__ __forceinline__ Half4 unpack4(const uint4 w) { return unpack4(w.x, w.y, w.z, w.w); }
-// ... from 4 floats
-template <bool SPLIT>
-__device__ __forceinline__ Half4 split4(const float4 f) {
-  const uint32_t h01 = pack_bf16(f.x, f.y), h23 = pack_bf16(f.z, f.w);
-  if (!SPLIT) return {h01, h23, 0u, 0u};
-  const uint32_t l01 = pack_bf16(f.x - __uint_as_float(h01 << 16), f.y - __uint_as_float(h01 & 0xFFFF0000u));
-  const uint32_t l23 = pack_bf16(f.z - __uint_as_float(h23 << 16), f.w - __uint_as_float(h23 & 0xFFFF0000u));
-  return {h01, h23, l01, l23};
-}
-constexpr Half4 kZero4 = {0u, 0u, 0u, 0u};
-
-__device__ __forceinline__ v8bf op_hi(const Half4 &a, const Half4 &b) {
-  return __builtin_bit_cast(v8bf, make_uint4(a.h01, a.h23, b.h01, b.h23));
-}
-__device__ __forceinline__ v8bf op_lo(const Half4 &a, const Half4 &b) {
-  return __builtin_bit_cast(v8bf, make_uint4(a.l01, a.l23, b.l01, b.l23));
-}
-
-// acc += A B for one 32-deep pair step (k blocks a0/b0 then a1/b1); the fp32 path adds the
-// hi*lo and lo*hi products.
-template <bool SPLIT>
-__device__ __forceinline__ v4f mma(const Half4 &a0, const Half4 &a1, const Half4 &b0, const Half4 &b1, v4f acc) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_hi(a0, a1), op_hi(b0, b1), acc, 0, 0, 0);
-  if (SPLIT) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_hi(a0, a1), op_lo(b0, b1), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_lo(a0, a1), op_hi(b0, b1), acc, 0, 0, 0);
-  }
-  return acc;
-}
 
 // 4 consecutive A values of the head (row r, columns c .. c + 3, c % 4 == 0), in bounds.
 template <bool U16>

@@ -1,0 +1,404 @@
+// GDN chunk recurrence (stage B of the chunked gated delta rule), C = 64, D = 128:
+// for every chunk of a (batch, head) sequence, in order, with the state S (D x D) carried,
+//     q^ = l2norm(q) / sqrt(D),  k^ = l2norm(k),  g = cumsum(gc) inside the chunk,
+//     P     = (q^ k^T) * e^{g_i - g_j}   (j <= i, else 0)
+//     v_new = U - W S
+//     o     = (q^ * e^g) S + P v_new
+//     S     = S e^{g_last} + (k^ * e^{g_last - g})^T v_new
+// from the stage-A outputs U = T (beta v) and W = T (beta k^ e^g)
+// (scripts/gdn_ref_kernel.py:66-69,91-101; the chunk loop :104-131).
+//
+// One workgroup (8 waves) per sequence walks its chunks.  S lives in registers for the whole
+// sequence: wave w owns S's value columns 16w .. 16w+15 as eight 16 x 16 MFMA result tiles,
+// which is also the layout the MFMA reads as a B operand over pairs of key blocks (pair layout,
+// bf16_split.h), so W S and q S take S straight from the accumulators.  q and k stay the bf16
+// values they arrive as (exact MFMA operands); their l2norm factors scale the products' rows and
+// columns instead.  Per chunk:
+//   L. q, k rows, k transposed and W (bf16 hi | lo words) into LDS; the row norms (8-lane DPP
+//      sums); g's prefix sum (64-lane DPP scan), e^g and e^{g_last - g} by one wave;
+//   M. each wave: W S and q S for its 16 value columns (4 token tiles), v_new = U - W S with U
+//      from registers, o's first term e^g q^ S; the 10 lower 16 x 16 tiles of q k^T over the
+//      waves, scaled by the norms and decays, into LDS as P;
+//   O. o = e^g q^ S + P v_new for the wave's columns (causal tiles only), stored;
+//   S. S = e^{g_last} S + k^T ((e^{g_last - g} / |k|) v_new), k^T from its transposed copy.
+// The next chunk's q, k, W, U and gc are read into registers during M, so their latency
+// overlaps this chunk's products; the workgroup issues them before its stores of o.
+// Precision: QH_GDN_FP32 carries W, S, P and v_new as bf16 hi/lo splits (hi*hi + hi*lo + lo*hi,
+// fp32 accumulation; products with the exact q, k take two terms); QH_GDN_BF16 uses the hi
+// parts only.  Norms, decays and the prefix sum are fp32.
+
+#include "bf16_split.h"
+#include "qmm_internal.h"
+
+namespace qh {
+namespace {
+
+using namespace bf16s;
+
+constexpr int kC = 64;          // chunk (tokens)
+constexpr int kD = 128;         // head dimension
+constexpr int kThreads = 512;   // 8 waves
+constexpr int kQs = kD + 8;     // LDS row stride of the q / k stores, bf16 (16-byte aligned rows)
+constexpr int kRs = kD + 4;     // LDS row stride of the W store, words
+constexpr int kPs = kC + 4;     // LDS row stride of P, words
+constexpr int kTs = kC + 4;     // LDS row stride of k^T, bf16 (8-byte aligned rows)
+
+struct StateArgs {
+  const uint16_t *q, *k;  // bf16 [B][T][H][D]
+  const float *g;         // [B][T][H] per-token log decays
+  const void *w, *u;      // [B][T][H][D] bf16 or fp32 (stage-A outputs, W in the e^g form)
+  const float *s_in;      // [B][H][D][D] or nullptr (zero state)
+  float *s_out;           // [B][H][D][D]
+  void *o;                // [B][T][H][D] bf16 or fp32
+  int B, T, H, nchunks;
+};
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ float bf16f(uint32_t h) { return __uint_as_float(h << 16); }
+
+// One chunk's inputs as read from global memory, per thread: the row segment (token t / 8,
+// columns 16 (t % 8) ..) of q, k and W, this wave's U tiles (MFMA result layout) and one gc
+// value per lane (every wave reads the same 64; wave 0 uses them).
+template <bool WU_F32>
+struct ChunkIn {
+  uint4 q[2], k[2];
+  uint4 w[WU_F32 ? 4 : 2];
+  float u[4][4];
+  float gc;
+};
+
+// Per-lane element offsets of chunk 0 (a chunk adds 64 H D): the thread's row segment, its
+// wave's U / o tile elements (token 4 qd + e of tile i is + (16 i + e) H D) and lane's gc.
+struct Offsets {
+  uint32_t row, tile, g;
+  uint32_t tok;  // H D: one token
+};
+
+__device__ __forceinline__ Offsets offsets(const StateArgs &a, int b, int h, int t, int wave, int lane) {
+  const int row = t >> 3, seg = t & 7, r16 = lane & 15, qd = lane >> 4;
+  const uint32_t tok = static_cast<uint32_t>(a.H) * kD;
+  const uint32_t seq = (static_cast<uint32_t>(b) * a.T * a.H + h) * kD;  // token 0 of the sequence
+  return {seq + row * tok + 16 * seg, seq + 4 * qd * tok + 16 * wave + r16,
+          static_cast<uint32_t>(b) * a.T * a.H + lane * a.H + h, tok};
+}
+
+template <bool WU_F32>
+__device__ __forceinline__ void load_chunk(const StateArgs &a, const Offsets &of, int n, ChunkIn<WU_F32> &in) {
+  const uint32_t c0 = static_cast<uint32_t>(n) * kC * of.tok;
+  const uint32_t ri = of.row + c0;
+  const uint4 *qp = reinterpret_cast<const uint4 *>(a.q + ri);
+  const uint4 *kp = reinterpret_cast<const uint4 *>(a.k + ri);
+  in.q[0] = qp[0];
+  in.q[1] = qp[1];
+  in.k[0] = kp[0];
+  in.k[1] = kp[1];
+  if constexpr (WU_F32) {
+    const uint4 *wp = reinterpret_cast<const uint4 *>(static_cast<const float *>(a.w) + ri);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) in.w[x] = wp[x];
+  } else {
+    const uint4 *wp = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.w) + ri);
+    in.w[0] = wp[0];
+    in.w[1] = wp[1];
+  }
+  const uint32_t ti = of.tile + c0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t ui = ti + static_cast<uint32_t>(16 * i + e) * of.tok;
+      in.u[i][e] = WU_F32 ? static_cast<const float *>(a.u)[ui] : bf16f(static_cast<const uint16_t *>(a.u)[ui]);
+    }
+  }
+  in.gc = a.g[of.g + static_cast<uint32_t>(n) * kC * static_cast<uint32_t>(a.H)];
+}
+
+// 8 bf16 values of a uint4 as floats.
+__device__ __forceinline__ void unbf16x8(const uint4 v, float *f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    f[2 * x] = bf16f(w[x] & 0xFFFFu);
+    f[2 * x + 1] = bf16f(w[x] >> 16);
+  }
+}
+
+// Lane move within a wave by DPP (CTRL: quad_perm 0x00-0xFF, row_shr:n 0x110+n, row_half_mirror
+// 0x141, row_bcast:15 0x142, row_bcast:31 0x143); lanes without a source, and rows outside
+// ROW_MASK, read 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over the 8 lanes 8r .. 8r+7: xor 1, xor 2 inside quads, then the mirrored quad.
+__device__ __forceinline__ float sum8(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  return x;
+}
+
+// Inclusive prefix sum over the 64 lanes: within rows of 16 by shifts 1, 2, 4, 8, then row 0's
+// total into row 1 and row 2's into row 3, then the first 32 lanes' total into rows 2 and 3.
+__device__ __forceinline__ float scan64(float x) {
+  x += dpp<0x111>(x);
+  x += dpp<0x112>(x);
+  x += dpp<0x114>(x);
+  x += dpp<0x118>(x);
+  x += dpp<0x142, 0xA>(x);
+  x += dpp<0x143, 0xC>(x);
+  return x;
+}
+
+// The 10 lower 16 x 16 tiles of P (token tile i >= j), two for waves 0 and 1.
+__device__ __forceinline__ void p_tile(int idx, int &i, int &j) {
+  i = idx < 1 ? 0 : idx < 3 ? 1 : idx < 6 ? 2 : 3;
+  j = idx - i * (i + 1) / 2;
+}
+
+// Four consecutive bf16 of an LDS row (8-byte aligned) as an exact operand half.
+__device__ __forceinline__ Half4 bf16x4(const uint16_t *p) {
+  const uint2 v = *reinterpret_cast<const uint2 *>(p);
+  return exact4(v.x, v.y);
+}
+template <bool SPLIT, bool WU_F32, bool OUT_F32>
+__global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
+  // q, k rows as given (bf16, exact MFMA operands) with their l2norm factors; W as hi | lo words;
+  // P as hi | lo words (lower tiles); g, e^g, e^{g_last - g} per token
+  __shared__ __attribute__((aligned(16))) uint16_t Ql[kC][kQs];
+  __shared__ __attribute__((aligned(16))) uint16_t Kl[kC][kQs];
+  __shared__ __attribute__((aligned(16))) uint16_t KlT[kD][kTs];  // k transposed: key, token
+  __shared__ __attribute__((aligned(16))) uint32_t Wl[kC][kRs];
+  __shared__ __attribute__((aligned(16))) uint32_t Pl[kC][kPs];
+  __shared__ float invq[kC], invk[kC];  // 1 / |q| / sqrt(D), 1 / |k| (eps 1e-6 inside the root)
+  __shared__ float gl[kC], egl[kC], decl[kC];
+  __shared__ float eglast;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int r16 = lane & 15, qd = lane >> 4;
+  const int b = blockIdx.x / a.H, h = blockIdx.x % a.H;
+
+  // S: tile kb holds rows (keys) 16 kb + 4 qd + e, column (value) 16 wave + r16
+  v4f S[8];
+  const size_t sbase = (static_cast<size_t>(b) * a.H + h) * kD * kD;
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      S[kb][e] = a.s_in ? a.s_in[sbase + static_cast<size_t>(16 * kb + 4 * qd + e) * kD + 16 * wave + r16] : 0.0f;
+  }
+
+  const Offsets of = offsets(a, b, h, t, wave, lane);
+  ChunkIn<WU_F32> in;
+  load_chunk<WU_F32>(a, of, 0, in);
+
+  for (int n = 0; n < a.nchunks; ++n) {
+    // ---- L: q, k, W into LDS; norms; g, e^g, e^{g_last - g} ------------------------------------
+    {
+      const int row = t >> 3, seg = t & 7;
+      *reinterpret_cast<uint4 *>(&Ql[row][16 * seg]) = in.q[0];
+      *reinterpret_cast<uint4 *>(&Ql[row][16 * seg + 8]) = in.q[1];
+      *reinterpret_cast<uint4 *>(&Kl[row][16 * seg]) = in.k[0];
+      *reinterpret_cast<uint4 *>(&Kl[row][16 * seg + 8]) = in.k[1];
+      {
+        const uint32_t kw[8] = {in.k[0].x, in.k[0].y, in.k[0].z, in.k[0].w, in.k[1].x, in.k[1].y, in.k[1].z, in.k[1].w};
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          KlT[16 * seg + 2 * x][row] = static_cast<uint16_t>(kw[x] & 0xFFFFu);
+          KlT[16 * seg + 2 * x + 1][row] = static_cast<uint16_t>(kw[x] >> 16);
+        }
+      }
+      float f[16];
+      unbf16x8(in.q[0], f);
+      unbf16x8(in.q[1], f + 8);
+      float ss = 0.0f;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) ss = fmaf(f[x], f[x], ss);
+      ss = sum8(ss);
+      if (seg == 0) invq[row] = (1.0f / sqrtf(ss + 1e-6f)) * (1.0f / 11.313708498984761f);  // then 1/sqrt(128)
+      unbf16x8(in.k[0], f);
+      unbf16x8(in.k[1], f + 8);
+      ss = 0.0f;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) ss = fmaf(f[x], f[x], ss);
+      ss = sum8(ss);
+      if (seg == 0) invk[row] = 1.0f / sqrtf(ss + 1e-6f);
+      if constexpr (WU_F32) {
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 4 * x]) =
+              make_uint4(hilo<SPLIT>(__uint_as_float(in.w[x].x)), hilo<SPLIT>(__uint_as_float(in.w[x].y)),
+                         hilo<SPLIT>(__uint_as_float(in.w[x].z)), hilo<SPLIT>(__uint_as_float(in.w[x].w)));
+      } else {  // bf16 W is exact: the hi part only
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const uint32_t w4[4] = {in.w[x].x, in.w[x].y, in.w[x].z, in.w[x].w};
+          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x]) =
+              make_uint4(w4[0] & 0xFFFFu, w4[0] >> 16, w4[1] & 0xFFFFu, w4[1] >> 16);
+          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x + 4]) =
+              make_uint4(w4[2] & 0xFFFFu, w4[2] >> 16, w4[3] & 0xFFFFu, w4[3] >> 16);
+        }
+      }
+      if (wave == 0) {
+        const float g = scan64(in.gc);
+        const float glast = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), 63));
+        gl[lane] = g;
+        egl[lane] = expf(g);
+        decl[lane] = expf(glast - g);
+        if (lane == 0) eglast = expf(glast);
+      }
+    }
+    float u[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u[i][e] = in.u[i][e];
+    }
+    lds_barrier();
+    if (n + 1 < a.nchunks) load_chunk<WU_F32>(a, of, n + 1, in);
+
+    // ---- M: W S, q^ S, v_new; P tiles ----------------------------------------------------------
+    Half4 sB[8];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) sB[kb] = split4<SPLIT>(S[kb]);
+    v4f ws[4], qs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ws[i] = qs[i] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {  // key blocks 2p, 2p + 1: 8 independent accumulations
+      const int c = 32 * p + 4 * qd;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t *wrow = Wl[16 * i + r16];
+        const uint16_t *qrow = Ql[16 * i + r16];
+        const Half4 w0 = unpack4(*reinterpret_cast<const uint4 *>(wrow + c));
+        const Half4 w1 = unpack4(*reinterpret_cast<const uint4 *>(wrow + c + 16));
+        ws[i] = WU_F32 ? mma<SPLIT>(w0, w1, sB[2 * p], sB[2 * p + 1], ws[i])
+                       : mma_exact_a<SPLIT>(w0, w1, sB[2 * p], sB[2 * p + 1], ws[i]);
+        qs[i] = mma_exact_a<SPLIT>(bf16x4(qrow + c), bf16x4(qrow + c + 16), sB[2 * p], sB[2 * p + 1], qs[i]);
+      }
+    }
+    v4f vnew[4], oacc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * i + 4 * qd + e;
+        vnew[i][e] = u[i][e] - ws[i][e];
+        oacc[i][e] = qs[i][e] * (invq[row] * egl[row]);
+      }
+    }
+    for (int idx = wave; idx < 10; idx += 8) {  // wave-uniform
+      int ti, tj;
+      p_tile(idx, ti, tj);
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t *qrow = Ql[16 * ti + r16];
+      const uint16_t *krow = Kl[16 * tj + r16];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int c = 32 * p + 4 * qd;
+        acc = mma<false>(bf16x4(qrow + c), bf16x4(qrow + c + 16), bf16x4(krow + c), bf16x4(krow + c + 16), acc);
+      }
+      const int col = 16 * tj + r16;
+      const float kf = invk[col];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * ti + 4 * qd + e;
+        const float pv = col <= row ? acc[e] * (invq[row] * kf) * expf(gl[row] - gl[col]) : 0.0f;
+        Pl[row][col] = hilo<SPLIT>(pv);
+      }
+    }
+    lds_barrier();
+
+    // ---- O: o = e^g q^ S + P v_new (causal pairs of token tiles) -------------------------------
+    Half4 vB[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vB[j] = split4<SPLIT>(vnew[j]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v4f acc = oacc[i];
+      const uint32_t *prow = Pl[16 * i + r16];
+#pragma unroll
+      for (int p = 0; p <= i / 2; ++p) {
+        const bool two = 2 * p + 1 <= i;
+        const int c = 32 * p + 4 * qd;
+        acc = mma<SPLIT>(unpack4(*reinterpret_cast<const uint4 *>(prow + c)),
+                         two ? unpack4(*reinterpret_cast<const uint4 *>(prow + c + 16)) : kZero4, vB[2 * p],
+                         two ? vB[2 * p + 1] : kZero4, acc);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t oi = of.tile + static_cast<uint32_t>(n * kC + 16 * i + e) * of.tok;
+        if (OUT_F32) {
+          static_cast<float *>(a.o)[oi] = acc[e];
+        } else {
+          static_cast<uint16_t *>(a.o)[oi] = static_cast<uint16_t>(pack_bf16(acc[e], 0.0f) & 0xFFFFu);
+        }
+      }
+    }
+
+    // ---- S: S = e^{g_last} S + k^T ((e^{g_last - g} / |k|) v_new) -------------------------------
+    Half4 dB[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v4f d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * j + 4 * qd + e;
+        d[e] = vnew[j][e] * (decl[row] * invk[row]);
+      }
+      dB[j] = split4<SPLIT>(d);
+    }
+    const float el = eglast;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[kb][e] *= el;
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {  // token blocks 2p, 2p + 1: 8 independent accumulations
+      const int c = 32 * p + 4 * qd;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        const uint16_t *krow = KlT[16 * kb + r16];  // key 16 kb + r16 = row of k^T
+        S[kb] = mma_exact_a<SPLIT>(bf16x4(krow + c), bf16x4(krow + c + 16), dB[2 * p], dB[2 * p + 1], S[kb]);
+      }
+    }
+    lds_barrier();  // the next chunk overwrites q, k, W, P and the decays
+  }
+
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      a.s_out[sbase + static_cast<size_t>(16 * kb + 4 * qd + e) * kD + 16 * wave + r16] = S[kb][e];
+  }
+}
+
+template <bool SPLIT, bool WU_F32, bool OUT_F32>
+qh_status launch3(const StateArgs &a, hipStream_t stream) {
+  hipLaunchKernelGGL((gdn_state_kernel<SPLIT, WU_F32, OUT_F32>), dim3(a.B * a.H), dim3(kThreads), 0, stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "gdn_state_kernel launch");
+  return QH_STATUS_OK;
+}
+
+template <bool SPLIT>
+qh_status launch2(const StateArgs &a, bool wu_f32, bool out_f32, hipStream_t stream) {
+  if (wu_f32) return out_f32 ? launch3<SPLIT, true, true>(a, stream) : launch3<SPLIT, true, false>(a, stream);
+  return out_f32 ? launch3<SPLIT, false, true>(a, stream) : launch3<SPLIT, false, false>(a, stream);
+}
+
+}  // namespace
+
+qh_status launch_gdn_chunk_state(const uint16_t *q, const uint16_t *k, const float *g, const void *w, const void *u,
+                                 const float *s_in, float *s_out, void *o, int B, int T, int H, int precision,
+                                 bool wu_f32, bool out_f32, hipStream_t stream) {
+  StateArgs a{q, k, g, w, u, s_in, s_out, o, B, T, H, T / kC};
+  return precision == QH_GDN_BF16 ? launch2<false>(a, wu_f32, out_f32, stream)
+                                  : launch2<true>(a, wu_f32, out_f32, stream);
+}
+
+}  // namespace qh

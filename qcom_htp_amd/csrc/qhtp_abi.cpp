@@ -249,4 +249,34 @@ qh_status qh_gdn_chunk_uw(const uint16_t *k_dev, const uint16_t *v_dev, const fl
                             0, stream);
 }
 
+qh_status qh_gdn_chunk_state(const uint16_t *q_dev, const uint16_t *k_dev, const float *g_dev, const void *w_dev,
+                             const void *u_dev, const float *s_in_dev, float *s_out_dev, void *o_dev, uint32_t batch,
+                             uint32_t tokens, uint32_t heads, uint32_t head_dim, uint32_t chunk, uint32_t flags,
+                             uint32_t precision, void *stream) {
+  if (!q_dev || !k_dev || !g_dev || !w_dev || !u_dev || !s_out_dev || !o_dev)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_state: NULL buffer");
+  if (head_dim != 128) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_state: head_dim=%u (need 128)", head_dim);
+  if (chunk != 64) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_state: chunk=%u (need 64)", chunk);
+  if (batch == 0 || heads == 0 || tokens == 0 || tokens % 64)
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_state: batch=%u tokens=%u heads=%u (tokens %% 64 == 0)",
+                batch, tokens, heads);
+  if (static_cast<uint64_t>(batch) * tokens * heads > (1ull << 31) / 128 ||
+      static_cast<uint64_t>(batch) * heads > (1u << 24))
+    return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_chunk_state: batch * tokens * heads too large");
+  if (flags & ~static_cast<uint32_t>(QH_GDN_OUT_F32 | QH_GDN_WU_F32))
+    return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_chunk_state: unknown flags 0x%x", flags);
+  if (precision > QH_GDN_BF16) return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_chunk_state: unknown precision %u", precision);
+  if (s_in_dev != nullptr && s_in_dev == s_out_dev)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_state: s_out_dev aliases s_in_dev");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(q_dev) | reinterpret_cast<uintptr_t>(k_dev) |
+                       reinterpret_cast<uintptr_t>(w_dev) | reinterpret_cast<uintptr_t>(u_dev) |
+                       reinterpret_cast<uintptr_t>(o_dev) | reinterpret_cast<uintptr_t>(s_out_dev) |
+                       reinterpret_cast<uintptr_t>(s_in_dev);
+  if (al % 16) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_chunk_state: buffers must be 16-byte aligned");
+  return launch_gdn_chunk_state(q_dev, k_dev, g_dev, w_dev, u_dev, s_in_dev, s_out_dev, o_dev, static_cast<int>(batch),
+                                static_cast<int>(tokens), static_cast<int>(heads), static_cast<int>(precision),
+                                (flags & QH_GDN_WU_F32) != 0, (flags & QH_GDN_OUT_F32) != 0,
+                                static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

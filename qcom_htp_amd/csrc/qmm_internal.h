@@ -168,4 +168,7 @@ qh_status launch_lpbq_expand(const uint8_t *codes, const uint8_t *scales, uint8_
                              hipStream_t stream);
 qh_status launch_gdn_chunk_uw(const uint16_t *k, const uint16_t *v, const float *g, const float *beta, void *w,
                               void *u, int B, int T, int H, int C, int flags, int max_wg, hipStream_t stream);
+qh_status launch_gdn_chunk_state(const uint16_t *q, const uint16_t *k, const float *g, const void *w, const void *u,
+                                 const float *s_in, float *s_out, void *o, int B, int T, int H, int precision,
+                                 bool wu_f32, bool out_f32, hipStream_t stream);
 }  // namespace qh

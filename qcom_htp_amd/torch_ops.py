@@ -15,6 +15,8 @@ HIP graph, each with a fake (meta) implementation for shape propagation:
 ``qhtp::gdn_solve``                T = (I - A)^-1 (fp32 / bf16-merge precision)
 ``qhtp::gdn_solve_u16``            the ``GdnSolve`` op's u16 code contract (GdnSolveOp.cpp:185-254)
 ``qhtp::gdn_chunk_uw``             the fused intra-chunk W, U products
+``qhtp::gdn_chunk_state``          the chunk recurrence (stage B): o and the final state
+``qhtp::gdn_prefill``              both stages, the reference's chunked ``gdn_kernel``
 =================================  ==================================================================
 
 A prepared matmul enters a graph as an integer handle (``register``): the weight re-layout is
@@ -26,6 +28,7 @@ from __future__ import annotations
 
 import itertools
 import threading
+from typing import Optional
 
 import torch
 from torch.library import custom_op
@@ -156,3 +159,35 @@ def gdn_chunk_uw(k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.
 def _(k, v, g, beta, chunk, decay_w=False, out_f32=False):
     dt = torch.float32 if out_f32 else torch.bfloat16
     return k.new_empty(k.shape, dtype=dt), k.new_empty(k.shape, dtype=dt)
+
+
+@custom_op("qhtp::gdn_chunk_state", mutates_args=())
+def gdn_chunk_state(q: torch.Tensor, k: torch.Tensor, g: torch.Tensor, w: torch.Tensor, u: torch.Tensor,
+                    initial_state: Optional[torch.Tensor] = None, precision: int = 0,
+                    out_f32: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    from .gdn import gdn_chunk_state as _state
+
+    return _state(q, k, g, w, u, initial_state, precision, torch.float32 if out_f32 else torch.bfloat16)
+
+
+@gdn_chunk_state.register_fake
+def _(q, k, g, w, u, initial_state=None, precision=0, out_f32=False):
+    B, T, H, D = q.shape
+    return (q.new_empty(q.shape, dtype=torch.float32 if out_f32 else torch.bfloat16),
+            q.new_empty((B, H, D, D), dtype=torch.float32))
+
+
+@custom_op("qhtp::gdn_prefill", mutates_args=())
+def gdn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                initial_state: Optional[torch.Tensor] = None, precision: int = 0,
+                out_f32: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    from .gdn import gdn_prefill as _prefill
+
+    return _prefill(q, k, v, g, beta, initial_state, precision, torch.float32 if out_f32 else torch.bfloat16)
+
+
+@gdn_prefill.register_fake
+def _(q, k, v, g, beta, initial_state=None, precision=0, out_f32=False):
+    B, T, H, D = q.shape
+    return (q.new_empty(q.shape, dtype=torch.float32 if out_f32 else torch.bfloat16),
+            q.new_empty((B, H, D, D), dtype=torch.float32))

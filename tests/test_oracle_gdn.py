@@ -139,3 +139,39 @@ def test_torch_stage_a_matches_lapack_products(decay_w):
     Uref, Wref = og.chunk_uw(og.inverse_fp64(og.build_A(k, beta, gc)), k, v, beta, gc, decay_w=decay_w)
     assert og.oc(U.numpy(), Uref) < 1e-12
     assert og.oc(W.numpy(), Wref) < 1e-12
+
+
+def _seq_inputs(n=3, T=100, D=16, seed=0):
+    rng = np.random.default_rng(seed)
+    q, k, v = (rng.standard_normal((n, T, D)) for _ in range(3))
+    gc = -np.logaddexp(0.0, -(rng.standard_normal((n, T)) + 3.0))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((n, T))))
+    return q, k, v, gc, beta
+
+
+@pytest.mark.parametrize("C", [16, 32, 64])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_chunked_prefill_equals_token_recurrence(C, with_state):
+    """The chunked stage A + stage B equals the gated delta rule applied token by token, for
+    every chunk size, with zero padding of a ragged T and with an incoming state."""
+    q, k, v, gc, beta = _seq_inputs()
+    S0 = np.random.default_rng(1).standard_normal((3, 16, 16)) * 0.1 if with_state else None
+    o_r, S_r = og.gdn_recurrent(q, k, v, gc, beta, S0)
+    o_c, S_c = og.gdn_prefill_torch(q, k, v, gc, beta, C, S0)
+    assert float((o_c - o_r).abs().max()) < 1e-12
+    assert float((S_c - S_r).abs().max()) < 1e-12
+
+
+def test_chunk_state_plausible_mistakes_are_caught():
+    """A dropped decay on the incoming state or a transposed state read changes the output."""
+    import torch
+
+    q, k, v, gc, beta = _seq_inputs(T=64)
+    o_r, _ = og.gdn_recurrent(q, k, v, gc, beta)
+    U, W = og.chunk_stage_a_torch(k.reshape(-1, 32, 16), v.reshape(-1, 32, 16), gc.reshape(-1, 32),
+                                  beta.reshape(-1, 32), decay_w=False)  # W without e^g: wrong form
+    o_bad, _ = og.chunk_state_torch(q, k, gc, W.reshape(3, 64, 16), U.reshape(3, 64, 16), None, 32)
+    assert float((o_bad - o_r).abs().max()) > 1e-3
+    o_ok, _ = og.gdn_prefill_torch(q, k, v, gc, beta, 32)
+    assert float((o_ok - o_r).abs().max()) < 1e-12
+    assert isinstance(o_ok, torch.Tensor)
