@@ -248,8 +248,12 @@ qh_status qh_w4_lpbq_expand_to_i8(const uint8_t *weight_lpbq_dev, const uint8_t 
 /* ------------------------------------------------------------------------------------ */
 
 typedef enum qh_gdn_precision {
-  QH_GDN_FP32 = 0, /* fp32 diagonal solves and fp32 MFMA merges (rel. Frobenius <= 1e-4)   */
-  QH_GDN_BF16 = 1, /* fp32 diagonal solves, bf16 MFMA merges with fp32 accumulation        */
+  QH_GDN_FP32 = 0,     /* fp32 diagonal solves; merges on bf16 hi/lo split MFMA products with
+                          fp32 accumulation (rel. Frobenius <= 1e-4)                           */
+  QH_GDN_BF16 = 1,     /* fp32 diagonal solves, bf16 MFMA merges with fp32 accumulation        */
+  QH_GDN_OP_MODEL = 2, /* qh_gdn_solve_u16 only, C <= 64: the GdnSolve op's own scalar model,
+                          code for code (gdn_solve_core.h:28-83): int16 diagonal solves at the
+                          internal scale 2/32767, float32 merges, lroundf requant             */
 } qh_gdn_precision;
 
 /* A_dev: float32 [heads][C][C] row-major, only the strictly lower triangle is read.
@@ -263,7 +267,9 @@ qh_status qh_gdn_solve_f32(const float *A_dev, float *T_dev, uint32_t heads, uin
 /* Quantized I/O contract of the reference's GdnSolve op and bare-metal gdnbm_solve
  * (example/gdn_native/solve_op/src/GdnSolveOp.cpp:185-254; baremetal/inc/gdnbm.idl:7-13):
  * A_dev uint16 codes [heads][C][C], A = (code - zpA) * sA; T_dev uint16 codes
- * T_code = clip(rint(T / sT) + zpT, 0, 65535), zeros (= zpT) above the diagonal. */
+ * T_code = clip(rint(T / sT) + zpT, 0, 65535), zeros (= zpT) above the diagonal.
+ * With QH_GDN_OP_MODEL (C <= 64): the op's codes exactly, A_int16 = (int16)(code - zpA) and
+ * T_code = (uint16)(clip(lroundf(T / sT), +-32767) + zpT) (GdnSolveOp.cpp:201-208). */
 qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t heads, uint32_t C, int32_t zpA,
                            int32_t zpT, float sA, float sT, uint32_t precision, void *stream);
 

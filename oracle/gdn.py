@@ -17,6 +17,14 @@ Functions and the reference lines they follow
                          substitution on int16 codes at sT = 2/32767 with int32 accumulation,
                          fp64 block merges): scripts/gdn_solve_int16_model.py:25-56 and
                          example/gdn_native/solve_op/gdn_solve_ref.c:19-69.
+* ``solve_int16_op``  -- the GdnSolve op's own scalar model (example/gdn_native/solve_op/src/
+                         gdn_solve_core.h:28-83, driven by GdnSolveOp.cpp:201-208): diagonal blocks
+                         by forward substitution on int16 codes at the fixed internal scale
+                         2/32767 with int32 accumulation and float32 requant (lroundf, clip
+                         +-32767), block merges in float32 in the op's loop order, output codes
+                         lroundf(T / sTout) clipped to +-maxc.  Every float32 operation is
+                         rounded separately (no fused multiply-add), in the op's order.
+* ``gdn_solve_op_u16`` -- the op's uint16 contract around it: A = code - zpA, T code + zpT.
 * ``chunk_uw``        -- U = T (beta * V), W = T (beta * K) [or T (beta * K * e^g)],
                          scripts/gdn_ref_kernel.py:88-89.
 * ``forward_subst_torch`` / ``chunk_stage_a_torch`` -- the same row recurrence and the whole
@@ -42,6 +50,9 @@ Pinning
   nilpotent Neumann series on small C.
 * ``solve_int16_blocks`` is pinned against the reference's own C model compiled from
   /root/reference (oracle/_ref/gdn_solve_ref, built by oracle/Makefile) on the same codes.
+* ``solve_int16_op`` is pinned code for code against the op's core compiled from
+  /root/reference (oracle/_ref/gdn_test_core: int8 output at sTout = 1/127), and its float T
+  against ``solve_int16_blocks`` (same algorithm in float64).
 * ``build_A`` is pinned by closed-form special cases (beta = 0 -> A = 0; orthogonal keys ->
   A = 0; a rank-one check on two tokens).
 * ``forward_subst_torch`` and ``chunk_stage_a_torch`` are pinned against LAPACK's inverse
@@ -66,6 +77,8 @@ __all__ = [
     "quantize_u16",
     "dequantize_u16",
     "solve_int16_blocks",
+    "solve_int16_op",
+    "gdn_solve_op_u16",
     "chunk_uw",
     "forward_subst_torch",
     "chunk_stage_a_torch",
@@ -175,6 +188,67 @@ def solve_int16_blocks(Aq: np.ndarray, sA: float, sT: float, BL: int = 16) -> np
         for j in range(i + 1):
             T[i * BL:(i + 1) * BL, j * BL:(j + 1) * BL] = blk[(i, j)]
     return T
+
+
+def _lroundf(v: np.ndarray) -> np.ndarray:
+    """C lroundf on float32 values: round half away from zero (evaluated in float64, where
+    |v| + 0.5 is exact)."""
+    v = np.asarray(v, np.float32).astype(np.float64)
+    return (np.sign(v) * np.floor(np.abs(v) + 0.5)).astype(np.int64)
+
+
+def solve_int16_op(Aq: np.ndarray, sA: float, sTout: float, maxc: float) -> np.ndarray:
+    """The GdnSolve op's scalar model on one head (gdn_solve_core.h:28-83): int16 codes Aq
+    [C, C] (C % 16 == 0, C <= 64) at scale sA -> output codes [C, C] (int64) at sTout, clipped to
+    +-maxc, zero above the diagonal.  float32 arithmetic, one rounding per operation."""
+    f32 = np.float32
+    A = np.asarray(Aq, np.int64)
+    C = A.shape[0]
+    BL, nb = 16, C // 16
+    sA, sTout, maxc = f32(sA), f32(sTout), f32(maxc)
+    sTi = f32(2.0) / f32(32767.0)
+    inv_sTi = f32(1.0) / sTi
+    inv_sTout = f32(1.0) / sTout
+    Tf = np.zeros((C, C), f32)
+    for b in range(nb):
+        Tb = np.zeros((BL, BL), np.int64)
+        d = A[b * BL:(b + 1) * BL, b * BL:(b + 1) * BL]
+        for i in range(BL):
+            acc = (d[i, :i][:, None] * Tb[:i, :]).sum(0) if i else np.zeros(BL, np.int64)
+            acc = (acc + 2 ** 31) % 2 ** 32 - 2 ** 31  # the core's int32 accumulator (two's complement)
+            ei = np.where(np.arange(BL) == i, inv_sTi, f32(0.0)).astype(f32)
+            v = (ei + (acc.astype(f32) * sA)).astype(f32)
+            Tb[i] = np.clip(_lroundf(v), -32767, 32767)
+        Tf[b * BL:(b + 1) * BL, b * BL:(b + 1) * BL] = (Tb.astype(f32) * sTi).astype(f32)
+    Af = A.astype(f32)
+    for j in range(nb):
+        for i in range(j + 1, nb):
+            acc = np.zeros((BL, BL), f32)
+            for k in range(j, i):
+                s = np.zeros((BL, BL), f32)
+                for m in range(BL):  # s += (A * sA) * Tf, left to right, one rounding each
+                    a = (Af[i * BL:(i + 1) * BL, k * BL + m] * sA).astype(f32)
+                    s = (s + (a[:, None] * Tf[k * BL + m, j * BL:(j + 1) * BL][None, :]).astype(f32)).astype(f32)
+                acc = (acc + s).astype(f32)
+            s = np.zeros((BL, BL), f32)
+            for m in range(BL):
+                s = (s + (Tf[i * BL:(i + 1) * BL, i * BL + m][:, None] * acc[m][None, :]).astype(f32)).astype(f32)
+            Tf[i * BL:(i + 1) * BL, j * BL:(j + 1) * BL] = s
+    q = np.clip(_lroundf((Tf * inv_sTout).astype(f32)), -int(maxc), int(maxc))
+    return np.tril(q)
+
+
+def gdn_solve_op_u16(Au: np.ndarray, zpA: int, sA: float, zpT: int, sT: float) -> np.ndarray:
+    """The op's uint16 contract per head (GdnSolveOp.cpp:201-208): A codes - zpA as int16, the
+    model with output scale sT and clip 32767, + zpT.  Au [..., C, C] uint16 -> uint16."""
+    Au = np.asarray(Au)
+    C = Au.shape[-1]
+    flat = Au.reshape(-1, C, C)
+    out = np.empty(flat.shape, np.uint16)
+    for h in range(flat.shape[0]):
+        As = (flat[h].astype(np.int64) - zpA).astype(np.int16)
+        out[h] = (solve_int16_op(As, sA, sT, 32767.0) + zpT).astype(np.uint16)
+    return out.reshape(Au.shape)
 
 
 def chunk_uw(T: np.ndarray, k: np.ndarray, v: np.ndarray, beta: np.ndarray, gc: np.ndarray, decay_w: bool = False):

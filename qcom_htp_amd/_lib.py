@@ -52,6 +52,7 @@ QH_CARRIER_BIASED = 4
 
 QH_GDN_FP32 = 0
 QH_GDN_BF16 = 1
+QH_GDN_OP_MODEL = 2
 
 QH_GDN_W_DECAY = 1
 QH_GDN_OUT_F32 = 2

@@ -203,12 +203,18 @@ qh_status qh_gdn_solve_u16(const uint16_t *A_dev, uint16_t *T_dev, uint32_t head
   if (A_dev == nullptr || T_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: NULL buffer");
   if (heads == 0 || heads > (1u << 24)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_u16: bad heads=%u", heads);
   if (C < 16 || C > 256 || C % 16) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_u16: C=%u (need 16..256, C%%16==0)", C);
-  if (precision > QH_GDN_BF16) return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_solve_u16: unknown precision %u", precision);
+  if (precision > QH_GDN_OP_MODEL)
+    return fail(QH_STATUS_UNSUPPORTED, "qh_gdn_solve_u16: unknown precision %u", precision);
   if (zpA < 0 || zpA > 65535 || zpT < 0 || zpT > 65535)
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: zero points must be in [0, 65535]");
   if (!(sA > 0.0f) || !(sT > 0.0f)) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: scales must be > 0");
   if (reinterpret_cast<uintptr_t>(A_dev) % 16 || reinterpret_cast<uintptr_t>(T_dev) % 16)
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_gdn_solve_u16: buffers must be 16-byte aligned");
+  if (precision == QH_GDN_OP_MODEL) {
+    if (C > 64) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_gdn_solve_u16: the op model takes C <= 64 (C=%u)", C);
+    return launch_gdn_solve_op_model(A_dev, T_dev, static_cast<int>(heads), static_cast<int>(C), zpA, zpT, sA, sT,
+                                     static_cast<hipStream_t>(stream));
+  }
   return launch_gdn_solve_u16(A_dev, T_dev, static_cast<int>(heads), static_cast<int>(C), zpA, zpT, sA, sT,
                               static_cast<int>(precision), static_cast<hipStream_t>(stream));
 }

@@ -164,6 +164,8 @@ qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, voi
 qh_status launch_gdn_solve_f32(const float *A, float *T, int heads, int C, int precision, hipStream_t stream);
 qh_status launch_gdn_solve_u16(const uint16_t *A, uint16_t *T, int heads, int C, int zpA, int zpT, float sA,
                                float sT, int precision, hipStream_t stream);
+qh_status launch_gdn_solve_op_model(const uint16_t *A, uint16_t *T, int heads, int C, int zpA, int zpT, float sA,
+                                    float sT, hipStream_t stream);
 qh_status launch_lpbq_expand(const uint8_t *codes, const uint8_t *scales, uint8_t *out, uint32_t K, uint32_t N,
                              hipStream_t stream);
 qh_status launch_gdn_chunk_uw(const uint16_t *k, const uint16_t *v, const float *g, const float *beta, void *w,

@@ -23,10 +23,12 @@ from . import _lib
 
 FP32 = _lib.QH_GDN_FP32
 BF16 = _lib.QH_GDN_BF16
+OP_MODEL = _lib.QH_GDN_OP_MODEL  # GdnSolve only: the reference op's own codes (C <= 64)
 
 W_DECAY = _lib.QH_GDN_W_DECAY
 
-__all__ = ["gdn_solve", "gdn_chunk_uw", "gdn_chunk_state", "gdn_prefill", "GdnSolve", "FP32", "BF16", "W_DECAY"]
+__all__ = ["gdn_solve", "gdn_chunk_uw", "gdn_chunk_state", "gdn_prefill", "GdnSolve", "FP32", "BF16", "OP_MODEL",
+           "W_DECAY"]
 
 
 def _stream(stream):
@@ -52,7 +54,8 @@ def gdn_solve(A: torch.Tensor, precision: int = FP32, out: Optional[torch.Tensor
 
 def GdnSolve(A_codes: torch.Tensor, zpA: int, sA: float, zpT: int, sT: float, precision: int = FP32,
              out: Optional[torch.Tensor] = None, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-    """uint16 codes A [B, H, C, C] -> uint16 codes T (the GdnSolve op contract)."""
+    """uint16 codes A [B, H, C, C] -> uint16 codes T (the GdnSolve op contract).  ``OP_MODEL``
+    (C <= 64) returns the op's own codes exactly (gdn_solve_core.h:28-83)."""
     if A_codes.device.type != "cuda" or A_codes.dtype != torch.uint16 or not A_codes.is_contiguous():
         raise TypeError("A_codes must be a contiguous uint16 CUDA tensor")
     C = A_codes.shape[-1]

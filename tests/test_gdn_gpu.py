@@ -171,3 +171,53 @@ def test_gdn_chunk_uw_rejects_bad_shapes(gpu):
         gdn_chunk_uw(k, k, g, g, 64)  # 96 tokens is not a multiple of the 64-token chunk
     with pytest.raises(_lib.QhtpError):
         gdn_chunk_uw(k, k, g, g, 32)  # unsupported chunk
+
+
+def _op_codes(A, sA):
+    return np.clip(np.rint(A / sA), -32767, 32767).astype(np.int64)
+
+
+@pytest.mark.parametrize("C", [16, 32, 48, 64])
+@pytest.mark.parametrize("case", ["config4", "zero", "full_range"])
+def test_gdn_op_model_codes_exact(gpu, C, case):
+    """QH_GDN_OP_MODEL returns the GdnSolve op's own uint16 codes (gdn_solve_core.h:28-83 via
+    GdnSolveOp.cpp:201-208), compared code for code with oracle.gdn.gdn_solve_op_u16, which is
+    pinned to the op core compiled from the reference."""
+    import torch
+
+    from qcom_htp_amd.gdn import OP_MODEL, GdnSolve
+
+    heads, zpA, zpT = 6, 32768, 32768
+    sT = float(np.float32(2.0 / 32767.0))
+    if case == "config4":
+        k, beta, gc = og.config4_inputs(heads=heads, C=C, seed=70 + C)
+        A = og.build_A(k, beta, gc)
+        sA = float(np.float32(np.abs(A).max() / 32767.0))
+        codes = _op_codes(A, sA)
+    elif case == "zero":
+        sA = 1e-4
+        codes = np.zeros((heads, C, C), np.int64)
+    else:  # full-range strictly-lower codes: clipping and int32 wrap-around paths
+        rng = np.random.default_rng(C)
+        codes = np.tril(rng.integers(-32767, 32768, (heads, C, C)), -1)
+        sA = 3e-5
+    Au = (codes + zpA).astype(np.uint16)
+    print(f"[gdn] op model C={C} case={case}", flush=True)
+    dev = torch.from_numpy(Au.view(np.int16)).to(gpu).view(torch.uint16)
+    T = GdnSolve(dev, zpA, sA, zpT, sT, precision=OP_MODEL)
+    torch.cuda.synchronize()
+    got = T.cpu().view(torch.int16).numpy().view(np.uint16)
+    want = og.gdn_solve_op_u16(Au, zpA, sA, zpT, sT)
+    diff = np.count_nonzero(got != want)
+    assert diff == 0, f"{diff} codes differ"
+
+
+def test_gdn_op_model_rejects_large_chunks(gpu):
+    import torch
+
+    from qcom_htp_amd import _lib
+
+    A = torch.zeros((1, 128, 128), dtype=torch.uint16, device=gpu)
+    st = _lib.lib().qh_gdn_solve_u16(A.data_ptr(), A.data_ptr(), 1, 128, 32768, 32768, 1e-4, 1e-4, 2,
+                                    int(torch.cuda.current_stream().cuda_stream))
+    assert st == _lib.QH_STATUS_SHAPE_UNSUPPORTED

@@ -175,3 +175,54 @@ def test_chunk_state_plausible_mistakes_are_caught():
     o_ok, _ = og.gdn_prefill_torch(q, k, v, gc, beta, 32)
     assert float((o_ok - o_r).abs().max()) < 1e-12
     assert isinstance(o_ok, torch.Tensor)
+
+
+@pytest.mark.skipif(not (REF_DIR / "gdn_test_core").exists(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("C", [16, 32, 64])
+def test_int16_op_model_matches_reference_core(tmp_path, C):
+    """solve_int16_op reproduces the op core's int8 output codes (gdn_solve_core.h through its
+    own host driver test_core.cpp, sTout = 1/127) code for code."""
+    H = 3
+    k, beta, gc = og.config4_inputs(heads=H, C=C, seed=17 + C)
+    A = og.build_A(k, beta, gc)
+    codes, sAs = [], []
+    for h in range(H):
+        q, s = _int16_codes(A[h])
+        codes.append(q)
+        sAs.append(s)
+    np.array([H, C], np.int32).tofile(tmp_path / "dims.i32")
+    np.stack(codes).astype(np.int16).tofile(tmp_path / "A_codes.i16")
+    np.array(sAs, np.float32).tofile(tmp_path / "sA.f32")
+    subprocess.run([str(REF_DIR / "gdn_test_core")], cwd=tmp_path, check=True, capture_output=True)
+    T_ref = np.fromfile(tmp_path / "T_i8.f64", np.float64).reshape(H, C, C)
+    sTout = np.float32(1.0) / np.float32(127.0)
+    ref_codes = np.rint(T_ref / np.float64(sTout)).astype(np.int64)
+    for h in range(H):
+        got = og.solve_int16_op(codes[h], float(np.float32(sAs[h])), float(sTout), 127.0)
+        assert np.array_equal(got, ref_codes[h]), f"head {h}: {np.count_nonzero(got != ref_codes[h])} codes differ"
+
+
+def test_int16_op_model_tracks_float64_block_model():
+    """The op's float32 model and the float64 block model are the same algorithm: their T agree
+    to float32 rounding (int16 output codes within one unit)."""
+    k, beta, gc = og.config4_inputs(heads=2, C=64, seed=23)
+    A = og.build_A(k, beta, gc)
+    sT = 2.0 / 32767.0
+    for h in range(2):
+        q, s = _int16_codes(A[h])
+        s32 = float(np.float32(s))
+        codes = og.solve_int16_op(q, s32, sT, 32767.0)
+        T64 = og.solve_int16_blocks(q, s32, float(np.float32(sT)))
+        assert np.abs(codes - np.clip(np.rint(T64 / sT), -32767, 32767)).max() <= 1
+        assert np.all(np.triu(codes, 1) == 0)
+
+
+def test_op_u16_contract_wraps_the_model():
+    """gdn_solve_op_u16 = model(codes - zpA) + zpT, zero (= zpT) above the diagonal."""
+    k, beta, gc = og.config4_inputs(heads=1, C=32, seed=29)
+    A = og.build_A(k, beta, gc)[0]
+    q, s = _int16_codes(A)
+    Au = (q.astype(np.int64) + 32768).astype(np.uint16)
+    out = og.gdn_solve_op_u16(Au[None], 32768, s, 32768, 2.0 / 32767.0)[0]
+    assert np.array_equal(out.astype(np.int64) - 32768, og.solve_int16_op(q, s, 2.0 / 32767.0, 32767.0))
+    assert np.all(out[np.triu_indices(32, 1)] == 32768)
