@@ -152,10 +152,17 @@ typedef enum qh_contract {
   QH_CONTRACT_ROUND_DIV = 4,         /* clip(round_half_away(acc / d) + out_zp, 0, qmax):        */
                                      /* hmx_w4a16_lpbq_scalar_native / round_div7               */
                                      /* (HmxU16I4ToU16MatMulOp.cpp:520-568, d = 7)               */
+  QH_CONTRACT_U8_DRAIN = 5,          /* clip(trunc(double(acc + bias_q) * s / 512) + (b >> 7),   */
+                                     /* 0, qmax): the closed-form A8 drain of                    */
+                                     /* scripts/reconstruct_hmx_u8_drain.py:10-16,153-156, with  */
+                                     /* act_zp = 128; `divisor` packs s as IEEE half bits (low   */
+                                     /* 16) and the u16 baseline b (high 16).  A reconstruction  */
+                                     /* of the hardware drain: no reference output pins it.      */
 } qh_contract;
 
 /* out_dev[M][N] (uint8 / uint16 per out_bits) = contract(acc) for act_dev[M][K]; exact int64
- * accumulation (i8 matrix cores), any M >= 1.  divisor >= 1 (ignored by the CLIP contracts).
+ * accumulation (i8 matrix cores), any M >= 1.  divisor >= 1 (ignored by the CLIP contracts;
+ * the packed drain parameters for QH_CONTRACT_U8_DRAIN, whose half scale must be finite).
  * Replaces the reference's integer reference steps and scalar LPBQ fallbacks listed above. */
 qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
                               uint32_t contract, uint32_t divisor, void *stream);

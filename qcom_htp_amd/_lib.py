@@ -30,6 +30,7 @@ QH_CONTRACT_CLIP_I64 = 1
 QH_CONTRACT_DIV_RINT = 2
 QH_CONTRACT_FLOOR256_DIV_RINT = 3
 QH_CONTRACT_ROUND_DIV = 4
+QH_CONTRACT_U8_DRAIN = 5
 QH_CONTRACT_NONE = 0xFFFFFFFF
 
 # Packed weight carriers (qh_weight_carrier) and their flags.

@@ -102,14 +102,18 @@ qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const voi
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: NULL buffer");
   if (reinterpret_cast<uintptr_t>(act_dev) % 16)
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: activation must be 16-byte aligned");
-  if (contract > QH_CONTRACT_ROUND_DIV)
+  if (contract > QH_CONTRACT_U8_DRAIN)
     return fail(QH_STATUS_UNSUPPORTED, "qh_qmm_run_contract: unknown contract %u", contract);
   const bool divides = contract == QH_CONTRACT_DIV_RINT || contract == QH_CONTRACT_FLOOR256_DIV_RINT ||
                        contract == QH_CONTRACT_ROUND_DIV;
   if (divides && (divisor == 0 || divisor > (1u << 30)))
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: divisor %u must be in [1, 2^30]", divisor);
+  if (contract == QH_CONTRACT_U8_DRAIN && ((divisor >> 10) & 31u) == 31u)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: drain scale 0x%04x is not a finite half",
+                divisor & 0xFFFFu);
+  const uint32_t param = divides || contract == QH_CONTRACT_U8_DRAIN ? divisor : 1u;
   return launch_qmm_exact(prep, static_cast<int>(m), act_dev, out_dev, 2, static_cast<int>(contract),
-                          divides ? static_cast<int>(divisor) : 1, static_cast<hipStream_t>(stream));
+                          static_cast<int>(param), static_cast<hipStream_t>(stream));
 }
 
 qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t chain, const void *act_dev,

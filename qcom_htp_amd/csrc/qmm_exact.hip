@@ -89,6 +89,15 @@ __device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, i
       const long long v = q + g.out_zp;
       return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
     }
+    case QH_CONTRACT_U8_DRAIN: {  // (acc + bias) * s / 512 in float64, truncated, + b >> 7
+      const uint32_t pk = static_cast<uint32_t>(g.divisor);
+      const uint32_t e = (pk >> 10) & 31u, f = pk & 1023u;
+      const double mag = e == 0 ? ldexp(static_cast<double>(f), -24) : ldexp(static_cast<double>(1024u + f), static_cast<int>(e) - 25);
+      const double s = (pk & 0x8000u) ? -mag : mag;
+      const long long drain = D + (g.bias_q ? g.bias_q[n] : 0);
+      const long long v = static_cast<long long>(trunc(static_cast<double>(drain) * s / 512.0)) + (pk >> 23);
+      return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
+    }
   }
   return 0;
 }

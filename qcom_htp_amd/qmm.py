@@ -42,6 +42,7 @@ CONTRACTS = {
     "div_rint": _lib.QH_CONTRACT_DIV_RINT,
     "floor256_div_rint": _lib.QH_CONTRACT_FLOOR256_DIV_RINT,
     "round_div": _lib.QH_CONTRACT_ROUND_DIV,
+    "u8_drain": _lib.QH_CONTRACT_U8_DRAIN,
 }
 
 

@@ -165,6 +165,31 @@ def test_contracts_match_oracle(gpu, fam):
     op.close()
 
 
+DRAIN_PARAMS = [(512.0, 0), (1.0, 32768), (2.0 ** -8, 16384), (-2.0, 0), (0.3, 0x1280), (2.0 ** -24, 65535)]
+
+
+@pytest.mark.parametrize("fam", ["u8i8", "w4a8_per_channel"])
+def test_u8_drain_contract_matches_oracle(gpu, fam):
+    """QH_CONTRACT_U8_DRAIN (the closed-form A8 drain, act_zp 128) against the oracle, several
+    half scales (normal, negative, subnormal) and baselines."""
+    import torch
+
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    c = C.synthetic_case(fam, 37, 256, 64, seed=23)
+    assert c.family.act_zp == 128
+    op = QuantMatmul.from_case(c, device=gpu)
+    act = torch.from_numpy(c.activation_q).to(gpu)
+    acc = oq.int_accumulator(c.activation_q, c.weight_int_nk, c.family.act_zp)
+    for scale, baseline in DRAIN_PARAMS:
+        d = int(np.array([scale], np.float16).view(np.uint16)[0]) | (baseline << 16)
+        print(f"[exact] {fam} u8 drain s={scale} b={baseline}", flush=True)
+        got = op.run_contract(act, "u8_drain", d).cpu().numpy()
+        want = oq.contract_output(acc, "u8_drain", d, c.bias_q, c.family.out_zp, c.family.out_bits)
+        assert np.array_equal(got, want), f"s={scale} b={baseline}: {diff_msg(got, want)}"
+    op.close()
+
+
 def test_contract_reference_models(gpu):
     """The reference's own integer models through the contracts: the legacy and native chain
     steps (gen_quant_chain.py:971-996), hmx_w4a16_lpbq_scalar_native (round_div7 on raw int4
