@@ -307,12 +307,17 @@ def _l2n(x):
     return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
 
 
-def chunk_state_torch(q, k, gc, W, U, S_in=None, C: int = 64):
+def chunk_state_torch(q, k, gc, W, U, S_in=None, C: int = 64, _plant: str = ""):
     """Stage B over whole sequences, torch float64 (scripts/gdn_ref_kernel.py:66-69,91-101).
 
     q, k [n, T, D] (raw; l2norm and 1/sqrt(D) applied here), gc [n, T] per-token log decays,
     W, U [n, T, D] the stage-A outputs of the same chunking (W in the T (beta k^ e^g) form),
-    S_in [n, D, D] or None.  Returns (o [n, T, D], S_out [n, D, D])."""
+    S_in [n, D, D] or None.  Returns (o [n, T, D], S_out [n, D, D]).
+
+    ``_plant`` (tests only) plants one plausible mistake, to show that the comparison against
+    the token recurrence catches it: "state_decay" (S not decayed by e^{g_last}), "transpose_S"
+    (S read transposed), "strict_causal" (P without its diagonal), "q_decay" (o's first term
+    without e^g), "k_decay" (the S update without e^{g_last - g})."""
     import torch
 
     f64 = torch.float64
@@ -323,24 +328,31 @@ def chunk_state_torch(q, k, gc, W, U, S_in=None, C: int = 64):
     kn = _l2n(k)
     S = torch.zeros(n, D, D, dtype=f64) if S_in is None else torch.as_tensor(S_in, dtype=f64).clone()
     o = torch.zeros(n, T, D, dtype=f64)
-    causal = torch.tril(torch.ones(C, C, dtype=torch.bool))
+    assert _plant in ("", "state_decay", "transpose_S", "strict_causal", "q_decay", "k_decay")
+    causal = torch.tril(torch.ones(C, C, dtype=torch.bool), diagonal=-1 if _plant == "strict_causal" else 0)
     for c0 in range(0, T, C):
         sl = slice(c0, c0 + C)
         g = torch.cumsum(gc[:, sl], dim=-1)
         decay = torch.exp(torch.where(causal, g.unsqueeze(-1) - g.unsqueeze(-2), torch.zeros((), dtype=f64))) * causal
         P = (qn[:, sl] @ kn[:, sl].transpose(-1, -2)) * decay
-        v_new = U[:, sl] - W[:, sl] @ S
-        o[:, sl] = (qn[:, sl] * torch.exp(g).unsqueeze(-1)) @ S + P @ v_new
+        Sr = S.transpose(-1, -2) if _plant == "transpose_S" else S
+        v_new = U[:, sl] - W[:, sl] @ Sr
+        qe = qn[:, sl] if _plant == "q_decay" else qn[:, sl] * torch.exp(g).unsqueeze(-1)
+        o[:, sl] = qe @ Sr + P @ v_new
         g_last = g[:, -1]
         dec = torch.exp(g_last.unsqueeze(-1) - g).unsqueeze(-1)
-        S = S * torch.exp(g_last)[:, None, None] + (kn[:, sl] * dec).transpose(-1, -2) @ v_new
+        if _plant == "k_decay":
+            dec = torch.ones_like(dec)
+        keep = torch.ones_like(g_last) if _plant == "state_decay" else torch.exp(g_last)
+        S = S * keep[:, None, None] + (kn[:, sl] * dec).transpose(-1, -2) @ v_new
     return o, S
 
 
-def gdn_prefill_torch(q, k, v, gc, beta, C: int = 64, S_in=None):
+def gdn_prefill_torch(q, k, v, gc, beta, C: int = 64, S_in=None, _plant: str = ""):
     """The reference's chunked prefill (scripts/gdn_ref_kernel.py:54-131) in torch float64 on
     [n, T, D] / [n, T] inputs: zero-pad T to whole chunks, stage A per chunk
-    (``chunk_stage_a_torch``, W in the e^g form), then stage B.  Returns (o [n, T, D], S)."""
+    (``chunk_stage_a_torch``, W in the e^g form), then stage B.  Returns (o [n, T, D], S).
+    ``_plant``: passed to ``chunk_state_torch`` (tests only)."""
     import torch
 
     f64 = torch.float64
@@ -354,7 +366,7 @@ def gdn_prefill_torch(q, k, v, gc, beta, C: int = 64, S_in=None):
     Tp = T + pad
     U, W = chunk_stage_a_torch(k.reshape(n * Tp // C, C, D), v.reshape(n * Tp // C, C, D),
                                gc.reshape(n * Tp // C, C), beta.reshape(n * Tp // C, C), decay_w=True)
-    o, S = chunk_state_torch(q, k, gc, W.reshape(n, Tp, D), U.reshape(n, Tp, D), S_in, C)
+    o, S = chunk_state_torch(q, k, gc, W.reshape(n, Tp, D), U.reshape(n, Tp, D), S_in, C, _plant)
     return o[:, :T], S
 
 

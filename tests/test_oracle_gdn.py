@@ -162,19 +162,24 @@ def test_chunked_prefill_equals_token_recurrence(C, with_state):
     assert float((S_c - S_r).abs().max()) < 1e-12
 
 
-def test_chunk_state_plausible_mistakes_are_caught():
-    """A dropped decay on the incoming state or a transposed state read changes the output."""
-    import torch
-
-    q, k, v, gc, beta = _seq_inputs(T=64)
-    o_r, _ = og.gdn_recurrent(q, k, v, gc, beta)
-    U, W = og.chunk_stage_a_torch(k.reshape(-1, 32, 16), v.reshape(-1, 32, 16), gc.reshape(-1, 32),
-                                  beta.reshape(-1, 32), decay_w=False)  # W without e^g: wrong form
-    o_bad, _ = og.chunk_state_torch(q, k, gc, W.reshape(3, 64, 16), U.reshape(3, 64, 16), None, 32)
-    assert float((o_bad - o_r).abs().max()) > 1e-3
-    o_ok, _ = og.gdn_prefill_torch(q, k, v, gc, beta, 32)
-    assert float((o_ok - o_r).abs().max()) < 1e-12
-    assert isinstance(o_ok, torch.Tensor)
+@pytest.mark.parametrize("plant", ["state_decay", "transpose_S", "strict_causal", "q_decay", "k_decay", "w_form"])
+def test_chunk_state_plausible_mistakes_are_caught(plant):
+    """Each plausible mistake planted in the chunked oracle (a dropped decay of the state, of q or
+    of k, a transposed state read, a causal mask without its diagonal, W without e^g) makes it
+    differ from the token-by-token recurrence, with an incoming state and over several chunks."""
+    q, k, v, gc, beta = _seq_inputs(T=96)
+    S0 = np.random.default_rng(2).standard_normal((3, 16, 16)) * 0.3
+    o_r, S_r = og.gdn_recurrent(q, k, v, gc, beta, S0)
+    if plant == "w_form":
+        U, W = og.chunk_stage_a_torch(k.reshape(-1, 32, 16), v.reshape(-1, 32, 16), gc.reshape(-1, 32),
+                                      beta.reshape(-1, 32), decay_w=False)
+        o_bad, S_bad = og.chunk_state_torch(q, k, gc, W.reshape(3, 96, 16), U.reshape(3, 96, 16), S0, 32)
+    else:
+        o_bad, S_bad = og.gdn_prefill_torch(q, k, v, gc, beta, 32, S0, _plant=plant)
+    err = max(float((o_bad - o_r).abs().max()), float((S_bad - S_r).abs().max()))
+    assert err > 1e-3, (plant, err)
+    o_ok, S_ok = og.gdn_prefill_torch(q, k, v, gc, beta, 32, S0)
+    assert float((o_ok - o_r).abs().max()) < 1e-12 and float((S_ok - S_r).abs().max()) < 1e-12
 
 
 @pytest.mark.skipif(not (REF_DIR / "gdn_test_core").exists(), reason="oracle/_ref not built (needs /root/reference)")
