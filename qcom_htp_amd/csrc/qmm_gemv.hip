@@ -86,6 +86,10 @@ __device__ __forceinline__ uint32_t resid4(uint32_t nb, const uint4 &tab) {
   return (pos & m) | (neg & ~m);
 }
 
+// Residue tables per column: one for each block scale f = 0 .. 16 (the LPBQ factor range; f = 0
+// serves the slots past K, whose codes are zero).
+constexpr int kRtabF = 17;
+
 // The residue table of (column n, block scale f): R(x) = fl32(x) - x for x = w M, computed as
 // the float32 conversion of the exact integer product (|x| < 2^31: |w| <= 112, M < 2^24), which
 // rounds like the float32 product w * s32 of the oracle.
@@ -327,7 +331,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   __shared__ int red[kGemvWaves][MM][16];
   __shared__ int red2[A16 ? kGemvWaves : 1][A16 ? MM : 1][16];
   __shared__ int red3[HR ? kGemvWaves : 1][HR ? MM : 1][16];
-  __shared__ uint4 rtab[HR ? 16 * 16 : 1];  // [column][block scale f]
+  __shared__ uint4 rtab[HR ? 16 * kRtabF : 1];  // [column][block scale f = 0 .. 16]
   __shared__ uint32_t r1[16];
   __shared__ uint16_t fix_list[MM * 16];
   __shared__ int fix_cnt;
@@ -414,8 +418,9 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   constexpr bool kMfma = MM == 16;
   for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
     if constexpr (HR) {
-      // residue tables of this group's 16 columns, one (column, f) per thread
-      rtab[t] = resid_table(static_cast<int>(g.mant[grp * 16 + (t >> 4)]), t & 15);
+      // residue tables of this group's 16 columns, one (column, f) per thread and step
+      for (int e = t; e < 16 * kRtabF; e += kGemvThreads)
+        rtab[e] = resid_table(static_cast<int>(g.mant[grp * 16 + e / kRtabF]), e % kRtabF);
       lds_barrier();
     }
     int acc[kMfma ? 1 : MM], acc2[A16 && !kMfma ? MM : 1], acc3[HR && !kMfma ? MM : 1];
@@ -445,7 +450,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
             const uint32_t f = valid ? (LPBQ ? ((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu : 1u) : 0u;
             const uint4 v = wv[i][0];
             if constexpr (HR) {
-              const uint4 tab = rtab[col * 16 + f];
+              const uint4 tab = rtab[col * kRtabF + f];
               rr[0] = resid4(v.x & 0x0F0F0F0Fu, tab); rr[1] = resid4(v.y & 0x0F0F0F0Fu, tab);
               rr[2] = resid4(v.z & 0x0F0F0F0Fu, tab); rr[3] = resid4(v.w & 0x0F0F0F0Fu, tab);
               rr[4] = resid4((v.x >> 4) & 0x0F0F0F0Fu, tab); rr[5] = resid4((v.y >> 4) & 0x0F0F0F0Fu, tab);
@@ -502,7 +507,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         const int f = LPBQ ? static_cast<int>(((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu) : 1;
         uint32_t rr[HR ? 8 : 1];  // residues of the 32 weights (zero codes in slots past K: r = 0)
         if constexpr (HR) {
-          const uint4 tab = rtab[col * 16 + (valid ? f : 0)];
+          const uint4 tab = rtab[col * kRtabF + (valid ? f : 0)];
 #pragma unroll
           for (int j = 0; j < 8; ++j) rr[j] = resid4(w[j], tab);
         }

@@ -88,6 +88,81 @@ def test_gemv_decode_rows_bit_exact(gpu, fam, rows):
     assert np.array_equal(got, want), diff_msg(got, want)
 
 
+@pytest.mark.parametrize("fam", ["w4a8_lpbq", "w4a16_lpbq"])
+@pytest.mark.parametrize("block", [32, 64])
+@pytest.mark.parametrize("rows", [1, 4, 6, 16])
+def test_gemv_lpbq_block_scale_16_bit_exact(gpu, fam, block, rows):
+    """LPBQ block scales over the reference's whole range [1, 16]: the factorisation gives 16 to a
+    column's largest group (generate_qnn_matmul_python_cases.py:189-200), which selects the last
+    entry of the per-(column, scale) tables of the 16-bit-activation GEMV."""
+    c = C.synthetic_case(fam, 16, 1024, 256, seed=41 + block, lpbq_block=block, lpbq_max_scale=16)
+    assert int(np.asarray(c.lpbq_block_int_scale).max()) == 16
+    print(f"[qmm] {fam} gemv block={block} scales<=16 rows={rows}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    want = oq.expected_output_case(c)[:rows]
+    assert np.array_equal(got, want), diff_msg(got, want)
+
+
+@pytest.mark.parametrize("fam", ["w4a8_lpbq", "w4a16_lpbq"])
+@pytest.mark.parametrize("rows", [1, 4, 6, 16])
+def test_gemv_block_scale_16_near_ties_bit_exact(gpu, fam, rows):
+    """Every block scale 16 and every row a near-tie row: weights 16 x code make the dot
+    product even, so an odd bias puts t half way between two outputs and the float32 rounding
+    residues of the weights decide the rounding."""
+    import dataclasses
+
+    from stress_cases import near_tie_case
+
+    c = near_tie_case(fam, 16, 512, 96, 13, tie_rows=list(range(16)))
+    codes = c.weight_q_nk.astype(np.int16)
+    c = dataclasses.replace(
+        c,
+        lpbq_block_int_scale=np.full_like(c.lpbq_block_int_scale, 16),
+        lpbq_expanded_q_nk=16 * codes,
+        weight_deq=(16 * codes).astype(np.float32) * np.asarray(c.weight_scale, np.float32)[:, None],
+    )
+    print(f"[qmm] {fam} gemv all block scales 16, near ties, rows={rows}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    want = oq.expected_output_case(c)[:rows]
+    assert np.array_equal(got, want), diff_msg(got, want)
+
+
+@pytest.mark.parametrize("rows", [1, 4, 6, 16])
+def test_gemv_block_scale_16_rail_activations_bit_exact(gpu, rows):
+    """16-bit activations on the rails (0 or 65535, so the high byte is +-128) with every block
+    scale 16: the high-byte rounding-residue sum the kernel forms exactly moves t by up to
+    0.005 output LSB, well beyond the low-byte margin, so a residue table read for the wrong
+    block scale changes outputs (2, 5, 5 and 12 of them at 1, 4, 6 and 16 rows for this seed)."""
+    import dataclasses
+
+    c = C.synthetic_case("w4a16_lpbq", 16, 1024, 2048, seed=3, lpbq_block=64, lpbq_max_scale=16)
+    codes = c.weight_q_nk.astype(np.int16)
+    rng = np.random.default_rng(103)
+    x = np.where(rng.random(c.activation_q.shape) < 0.5, 0, 65535).astype(np.uint16)
+    c = dataclasses.replace(
+        c,
+        activation_q=x,
+        lpbq_block_int_scale=np.full_like(c.lpbq_block_int_scale, 16),
+        lpbq_expanded_q_nk=16 * codes,
+        weight_deq=(16 * codes).astype(np.float32) * np.asarray(c.weight_scale, np.float32)[:, None],
+    )
+    print(f"[qmm] w4a16_lpbq gemv rail activations, block scales 16, rows={rows}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    want = oq.expected_output_case(c)[:rows]
+    assert np.array_equal(got, want), diff_msg(got, want)
+
+
+@pytest.mark.parametrize("fam", ["w4a8_lpbq", "w4a16_lpbq"])
+@pytest.mark.parametrize("rows", [1, 16])
+def test_gemv_single_k_impulse_bit_exact(gpu, fam, rows):
+    """The reference's single_k_impulse case (block scales up to 16) on the decode path."""
+    c = C.make_case(fam, "single_k_impulse", 256, 256, 256)
+    print(f"[qmm] {fam} single_k_impulse gemv rows={rows}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    want = oq.expected_output_case(c)[:rows]
+    assert np.array_equal(got, want), diff_msg(got, want)
+
+
 @pytest.mark.parametrize("fam", C.GATED_FAMILIES)
 def test_accumulators_exact(gpu, fam):
     import torch
