@@ -169,7 +169,7 @@ qh_status qh_qmm_release(qh_qmm_prepared *prep) {
   void *ptrs[] = {D.tiles, D.gemv_tiles, D.gemv_lpbq, D.alpha, D.beta, D.corr,
                   D.margin, D.absb, D.bias_deq, D.s32, D.mant, D.colsum, D.gemv_margin_r1,
                   D.colsum_r, D.alpha_e, D.scale_exp, D.margin_exact, D.resid, D.bias_q,
-                  D.corr_int, D.mult, D.corr_rq, D.s32g, D.margin_lo};
+                  D.corr_int, D.mult, D.corr_rq, D.s32g, D.margin_lo, D.lpbq_nk, D.gemv_rec};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   (void)hipSetDevice(cur);

@@ -55,6 +55,20 @@ __host__ __device__ inline size_t gemv_scale_index_kg(int n, int kg, int nbatch,
                           n % 16, j >> 4);
 }
 
+// Per-output-channel epilogue record of the int4 decode GEMV (qmm_gemv_unit.hip): everything its
+// requantisation and exact fixup read about a column, 96 bytes (six 16-byte pieces).
+struct GemvRec {
+  double alpha, beta, margin, absb;  // as QmmDevice
+  int64_t corr;                      // 8-bit acts: corr; 16-bit acts: colsum (sum_k w_int)
+  double mlo;                        // 16-bit acts: margin_lo; 8-bit acts: residue bound per unit of |a - zp|_2
+  int64_t mant, colsum_r;            // M of s32 = M 2^E; sum_k r_k
+  double bias_deq;
+  double alpha_e, margin_exact;      // as QmmDevice
+  float s32;
+  int32_t pad;
+};
+static_assert(sizeof(GemvRec) == 96, "GemvRec is six 16-byte pieces");
+
 // Everything the GEMM / GEMV kernels read, resident on the device.
 struct QmmDevice {
   // Weight operand tiles (GEMM).  For 16-bit activations the operand has 2N columns:
@@ -65,6 +79,8 @@ struct QmmDevice {
   // (int4 byte j: k = j in the low nibble, k = j + 16 in the high nibble, offset-binary).
   uint8_t *gemv_tiles;
   uint8_t *gemv_lpbq;   // LPBQ block scales for the GEMV stream (gemv_scale_index layout)
+  uint8_t *lpbq_nk;     // LPBQ block scales in the descriptor's [N][K / block] order (int4 GEMV)
+  GemvRec *gemv_rec;    // [N] (int4 weights)
   // Per output channel epilogue constants.
   double *alpha;    // t = fma(S, alpha, beta): S is the exact integer dot product
   double *beta;     //   (alpha = sA * s32 / sO for 8-bit acts, sA * 2^E / sO for 16-bit)
@@ -155,6 +171,9 @@ qh_status hip_fail(hipError_t err, const char *what);
 // Kernel launchers (defined in the .hip files).
 qh_status launch_qmm_gemm(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
 qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
+// The persistent int4 decode GEMV for M <= 4; returns QH_STATUS_SHAPE_UNSUPPORTED (without
+// launching or recording an error) for the shapes it does not take.
+qh_status launch_qmm_gemv_unit(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
 bool gemv_fits(const qh_qmm_prepared *p, int m);  // the GEMV's LDS staging holds M x K
 qh_status launch_qmm_accumulate(const qh_qmm_prepared *p, int m, const void *act, int64_t *acc,
                                 hipStream_t stream);

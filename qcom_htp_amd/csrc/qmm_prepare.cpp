@@ -297,7 +297,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   std::vector<int8_t> resid(static_cast<size_t>(N) * K);
   std::vector<int64_t> mant(N), colsum_q(N), colsum_r(N);
   std::vector<int> expo(N), rmax(N);
-  std::vector<double> r1(N), wpmax(N);
+  std::vector<double> r1(N), r2(N), wpmax(N);
   for (int n = 0; n < N; ++n) {
     const float s = d->weight_scale[n];
     if (!(s > 0.0f) || !std::isfinite(s) || s < std::numeric_limits<float>::min())
@@ -308,7 +308,7 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     mant[n] = M;
     expo[n] = E;
     int64_t cq = 0, cr = 0;
-    double ra = 0, wm = 0;
+    double ra = 0, rs = 0, wm = 0;
     int rm = 0;
     for (int k = 0; k < K; ++k) {
       int q = d->weight_nk[static_cast<size_t>(n) * K + k];
@@ -333,12 +333,14 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
       cq += w;
       cr += r;
       ra += std::fabs(static_cast<double>(r));
+      rs += static_cast<double>(r) * static_cast<double>(r);
       rm = std::max(rm, static_cast<int>(std::llabs(r)));
       wm = std::max(wm, std::fabs(wp));
     }
     colsum_q[n] = cq;
     colsum_r[n] = cr;
     r1[n] = ra;
+    r2[n] = rs;
     rmax[n] = rm;
     wpmax[n] = wm;
   }
@@ -485,6 +487,32 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
     corr_int[n] = static_cast<int64_t>((a16 ? 32896 : 128) - d->act_zp) * colsum_q[n];
   }
 
+  // ---- int4 decode GEMV: per-column records and the block scales in [N][K / block] order ------
+  std::vector<GemvRec> gemv_rec;
+  std::vector<uint8_t> lpbq_nk;
+  if (sh.gemv_fmt == kTileI4) {
+    gemv_rec.resize(N);
+    for (int n = 0; n < N; ++n) {
+      GemvRec &r = gemv_rec[n];
+      r.alpha = alpha[n];
+      r.beta = beta[n];
+      r.margin = margin[n];
+      r.absb = absb[n];
+      r.corr = a16 ? colsum_q[n] : corr[n];
+      // 16-bit acts: margin_lo.  8-bit acts: the Cauchy-Schwarz bound of the residue term per unit
+      // of |a - zp|_2 (|sum_k (a_k - zp) r_k| <= |a - zp|_2 |r|_2), in output LSB.
+      r.mlo = a16 ? mlo[n] : inv_sO * sA * std::ldexp(1.0, expo[n]) * std::sqrt(r2[n]) * kSafety;
+      r.mant = mant[n];
+      r.colsum_r = colsum_r[n];
+      r.bias_deq = bdeq[n];
+      r.alpha_e = alpha_e[n];
+      r.margin_exact = margin_exact[n];
+      r.s32 = s32v[n];
+      r.pad = 0;
+    }
+    if (lpbq) lpbq_nk.assign(d->lpbq_block_scale, d->lpbq_block_scale + static_cast<size_t>(N) * nblk);
+  }
+
   // ---- upload -------------------------------------------------------------------------------
   auto *p = new qh_qmm_prepared();
   p->shape = sh;
@@ -498,6 +526,8 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
   if (st == QH_STATUS_OK) st = al.upload(&D.tiles, tiles);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_tiles, gemv_tiles);
   if (st == QH_STATUS_OK) st = al.upload(&D.gemv_lpbq, gemv_lpbq);
+  if (st == QH_STATUS_OK) st = al.upload(&D.lpbq_nk, lpbq_nk);
+  if (st == QH_STATUS_OK) st = al.upload(&D.gemv_rec, gemv_rec);
   if (st == QH_STATUS_OK) st = al.upload(&D.alpha, alpha);
   if (st == QH_STATUS_OK) st = al.upload(&D.beta, beta);
   if (st == QH_STATUS_OK) st = al.upload(&D.corr, corr);
