@@ -50,6 +50,8 @@ struct GemvArgs {
   const float *s32;
   int M, N, K, KG, nbatch, sub_shift;
   int act_zp, out_zp, out_qmax, out16;
+  int ars;       // LDS row stride of the staged activation planes, bytes: K + 16 (the 16 rows
+                 // one 16-byte read instruction spans then fall on distinct banks)
   int off_asum;  // byte offset of the k-group sums in dynamic LDS
   int off_fixw;  // byte offset of the fixup columns' weight words (register-held fixup)
   double sA, sO;
@@ -82,8 +84,8 @@ __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, 
       wd[4 * q] = v.x; wd[4 * q + 1] = v.y; wd[4 * q + 2] = v.z; wd[4 * q + 3] = v.w;
     }
     const int f = LPBQ ? g.lpbq[gemv_scale_index_kg(n, kg, g.nbatch, g.sub_shift)] : 1;
-    const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * K + kg * 32);
-    const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * K + kg * 32);
+    const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
+    const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * g.ars + kg * 32);
 #pragma unroll 4
     for (int j = 0; j < 32; ++j) {
       int w;
@@ -142,8 +144,8 @@ __device__ void gemv_fixup_batch(const GemvArgs &g, const uint8_t *lds, const ui
                                                        (FMT == kTileI4 ? 0 : 16 * h));
       const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
       const int f = LPBQ ? fixs[e * KG + kg] : 1;
-      const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(mrow[e]) * K + kg * 32 + 16 * h);
-      const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + mrow[e]) * K + kg * 32 + 16 * h);
+      const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(mrow[e]) * g.ars + kg * 32 + 16 * h);
+      const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + mrow[e]) * g.ars + kg * 32 + 16 * h);
 #pragma unroll 4
       for (int j = 0; j < 16; ++j) {
         const uint32_t byte = (wd[j >> 2] >> (8 * (j & 3))) & 0xFFu;
@@ -204,7 +206,7 @@ __device__ __forceinline__ void store_unit(const GemvArgs &g, int u, ActUnit<A16
     uint4 v0 = r.v[0], v1 = r.v[A16 ? 1 : 1];
     v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
     v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
-    uint4 *dst = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(m) * K + kg * 32);
+    uint4 *dst = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
     dst[0] = v0;
     dst[1] = v1;
     if (FMT == kTileI4) {
@@ -228,8 +230,8 @@ __device__ __forceinline__ void store_unit(const GemvArgs &g, int u, ActUnit<A16
       lv[2 * q] = perm(v.y, v.x, 0x06040200u);
       lv[2 * q + 1] = perm(v.w, v.z, 0x06040200u);
     }
-    uint4 *dh = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(m) * K + kg * 32);
-    uint4 *dl = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(M + m) * K + kg * 32);
+    uint4 *dh = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
+    uint4 *dl = reinterpret_cast<uint4 *>(lds + static_cast<size_t>(M + m) * g.ars + kg * 32);
     dh[0] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
     dh[1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
     dl[0] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
@@ -394,19 +396,24 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
             b[0] = v0.x & mk; b[1] = v0.y & mk; b[2] = v0.z & mk; b[3] = v0.w & mk;
             b[4] = v1.x & mk; b[5] = v1.y & mk; b[6] = v1.z & mk; b[7] = v1.w & mk;
           }
-          const uint2 *ap = reinterpret_cast<const uint2 *>(lds + static_cast<size_t>(mrow) * K + kg * 32);
+          // 16-byte reads: with the padded row stride the 16 rows of a quarter hit distinct banks
+          const uint4 *ap4 = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(mrow) * g.ars + kg * 32);
+          const uint4 ah0 = ap4[0], ah1 = ap4[1];
+          const uint2 ah[4] = {make_uint2(ah0.x, ah0.y), make_uint2(ah0.z, ah0.w), make_uint2(ah1.x, ah1.y), make_uint2(ah1.z, ah1.w)};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const uint2 a = ap[j];
+            const uint2 a = ah[j];
             macc = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(b[2 * j], b[2 * j + 1]), macc, 0, 0, 0);
             if constexpr (HR)
               macc3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(rr[2 * j], rr[2 * j + 1]), macc3, 0, 0, 0);
           }
           if (A16) {
-            const uint2 *lp = reinterpret_cast<const uint2 *>(lds + static_cast<size_t>(M + mrow) * K + kg * 32);
+            const uint4 *lp4 = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(M + mrow) * g.ars + kg * 32);
+            const uint4 al0 = lp4[0], al1 = lp4[1];
+            const uint2 al[4] = {make_uint2(al0.x, al0.y), make_uint2(al0.z, al0.w), make_uint2(al1.x, al1.y), make_uint2(al1.z, al1.w)};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const uint2 a = lp[j];
+              const uint2 a = al[j];
               macc2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(b[2 * j], b[2 * j + 1]), macc2, 0, 0, 0);
             }
           }
@@ -441,7 +448,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
           if (MM > 1 && m >= M) continue;
-          const uint4 *ap = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(m) * K + kg * 32);
+          const uint4 *ap = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
           const uint4 a0 = ap[0], a1 = ap[1];
           int d = sdot4(a0.x, w[0], 0);
           d = sdot4(a0.y, w[1], d); d = sdot4(a0.z, w[2], d); d = sdot4(a0.w, w[3], d);
@@ -449,7 +456,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
           if (FMT == kTileI4) d -= a8 * asum[m * KG + kg];
           acc[m] += LPBQ ? d * f : d;
           if (A16) {
-            const uint4 *lp = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(M + m) * K + kg * 32);
+            const uint4 *lp = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(M + m) * g.ars + kg * 32);
             const uint4 b0 = lp[0], b1 = lp[1];
             int e = sdot4(b0.x, w[0], 0);
             e = sdot4(b0.y, w[1], e); e = sdot4(b0.z, w[2], e); e = sdot4(b0.w, w[3], e);
@@ -634,7 +641,7 @@ GemvLds gemv_lds(const QmmShape &sh, int m) {
   const int KG = sh.K / 32;
   const int WB = sh.gemv_fmt == kTileI4 ? 16 : 32;
   GemvLds L;
-  L.off_asum = align16(static_cast<size_t>(planes) * m * sh.K);
+  L.off_asum = align16(static_cast<size_t>(planes) * m * (sh.K + 16));
   const size_t asum_bytes = sh.gemv_fmt == kTileI4 ? static_cast<size_t>(planes) * m * KG * 2 : 0;
   L.off_fixw = align16(L.off_asum + asum_bytes);
   // (only single-group launches, M <= 4, with one batch of k-groups hold the weights)
@@ -693,6 +700,7 @@ qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void
   g.out_zp = sh.out_zp;
   g.out_qmax = (1 << sh.out_bits) - 1;
   g.out16 = sh.out_bits == 16;
+  g.ars = sh.K + 16;
   g.off_asum = static_cast<int>(off_asum);
   g.off_fixw = static_cast<int>(off_fixw);
   g.sA = sh.act_scale;
