@@ -70,7 +70,7 @@ template <bool A16, int FMT, bool LPBQ>
 __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, int lane) {
   constexpr int WB = FMT == kTileI4 ? 16 : 32;
   const float sc = g.s32[n];
-  const int K = g.K, KG = g.KG;
+  const int KG = g.KG;
   const uint8_t *const wcol = g.w + (static_cast<size_t>(n / 16) * KG * 16 + (n % 16)) * WB;
   // a - zp = plane value + off (8-bit: a - 128; 16-bit: 256 hi + lo' with a - 32768 - 128)
   const int off = (A16 ? 32768 + 128 : 128) - g.act_zp;
@@ -123,7 +123,7 @@ template <bool A16, int FMT, bool LPBQ>
 __device__ void gemv_fixup_batch(const GemvArgs &g, const uint8_t *lds, const uint8_t *fixw, const uint8_t *fixs,
                                  double *dred, const uint16_t *list, int nb, int grp, int t) {
   constexpr int WB = FMT == kTileI4 ? 16 : 32;
-  const int K = g.K, KG = g.KG;
+  const int KG = g.KG;
   const int off = (A16 ? 32768 + 128 : 128) - g.act_zp;
   double s[kFixBatch];
   float sc[kFixBatch];
@@ -199,7 +199,7 @@ __device__ __forceinline__ void load_unit(const GemvArgs &g, int u, ActUnit<A16>
 
 template <bool A16, int FMT>
 __device__ __forceinline__ void store_unit(const GemvArgs &g, int u, ActUnit<A16> r, uint8_t *lds, uint32_t *r1) {
-  const int M = g.M, K = g.K, KG = g.KG;
+  const int M = g.M, KG = g.KG;
   const int m = u / KG, kg = u - m * KG;
   int16_t *asum = reinterpret_cast<int16_t *>(lds + g.off_asum);
   if (!A16) {
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   __shared__ double dred[kFixBatch * kGemvWaves];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int M = g.M, K = g.K, KG = g.KG;
+  const int M = g.M, KG = g.KG;
   constexpr int WB = FMT == kTileI4 ? 16 : 32;  // stream bytes per (column, k-group)
   const int16_t *const asum = reinterpret_cast<const int16_t *>(lds + g.off_asum);
   const int col = lane & 15, sub = lane >> 4;
@@ -615,18 +615,45 @@ qh_status launch_one(const GemvArgs &g, dim3 grid, size_t dyn_lds, hipStream_t s
   return QH_STATUS_OK;
 }
 
+// Workgroups of the 16-row kernel that are resident at once with dyn_lds bytes of dynamic LDS
+// (occupancy x compute units), or 0 if the runtime cannot say.  Cached for the last query.
+template <bool A16, int FMT, bool LPBQ>
+int resident_workgroups(size_t dyn_lds) {
+  static std::atomic<uint64_t> last{0};  // dyn_lds << 24 | device << 16 | workgroups
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev > 255) return 0;
+  const uint64_t key = (static_cast<uint64_t>(dyn_lds) << 24) | (static_cast<uint64_t>(dev) << 16);
+  const uint64_t hit = last.load(std::memory_order_acquire);
+  if ((hit & ~static_cast<uint64_t>(0xFFFF)) == key && (hit & 0xFFFF) != 0) return static_cast<int>(hit & 0xFFFF);
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(&qmm_gemv_kernel<A16, FMT, LPBQ, 16>),
+                                                   kGemvThreads, dyn_lds) != hipSuccess)
+    return 0;
+  const long long wg = static_cast<long long>(occ) * device_cu_count();
+  if (wg <= 0 || wg > 0xFFFF) return 0;
+  last.store(key | static_cast<uint64_t>(wg), std::memory_order_release);
+  return static_cast<int>(wg);
+}
+
 template <bool A16, int FMT, bool LPBQ>
 qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
   const int groups = g.N / 16;
-  // One group per workgroup while the staged activations are small; larger staging is
-  // amortised over several groups per workgroup.
+  // One group per workgroup while the staged activations are small.  Larger staging is
+  // amortised over several groups per workgroup: at most 512 workgroups, and no more than are
+  // resident at once, since a second round would stage the activations again (16 rows of
+  // 16-bit activations at K = 4096 take 128 KiB, one workgroup per compute unit).
+  if (g.M <= 1) return launch_one<A16, FMT, LPBQ, 1>(g, dim3(groups), dyn_lds, stream);
+  if (g.M <= 4) return launch_one<A16, FMT, LPBQ, 4>(g, dim3(groups), dyn_lds, stream);
   const int planes = A16 ? 2 : 1;
   int blocks = groups;
-  if (g.M > 4 && static_cast<size_t>(planes) * g.M * g.K > 16384 && blocks > 512) blocks = 512;
-  const dim3 grid(blocks);
-  if (g.M <= 1) return launch_one<A16, FMT, LPBQ, 1>(g, grid, dyn_lds, stream);
-  if (g.M <= 4) return launch_one<A16, FMT, LPBQ, 4>(g, grid, dyn_lds, stream);
-  return launch_one<A16, FMT, LPBQ, 16>(g, grid, dyn_lds, stream);
+  if (static_cast<size_t>(planes) * g.M * g.K > 16384) {
+    const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, 16>();  // before the occupancy query
+    if (st != QH_STATUS_OK) return st;
+    const int cap = resident_workgroups<A16, FMT, LPBQ>(dyn_lds);
+    const int lim = cap > 0 && cap < 512 ? cap : 512;
+    if (blocks > lim) blocks = lim;
+  }
+  return launch_one<A16, FMT, LPBQ, 16>(g, dim3(blocks), dyn_lds, stream);
 }
 
 size_t align16(size_t x) { return (x + 15) & ~static_cast<size_t>(15); }

@@ -554,17 +554,7 @@ __global__ __launch_bounds__(kUT, 1) void qmm_gemv_unit_kernel(const UnitArgs g)
 
 size_t al16(size_t x) { return (x + 15) & ~static_cast<size_t>(15); }
 
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
+int cu_count() { return device_cu_count(); }
 
 template <bool A16, bool LPBQ, int MM, int S>
 qh_status launch_unit(const UnitArgs &g, size_t dyn, hipStream_t stream) {
@@ -594,6 +584,18 @@ qh_status launch_s(const UnitArgs &g, int S, size_t dyn, hipStream_t stream) {
 }
 
 }  // namespace
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 qh_status launch_qmm_gemv_unit(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream) {
   const QmmShape &sh = p->shape;

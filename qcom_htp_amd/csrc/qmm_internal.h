@@ -173,6 +173,8 @@ qh_status launch_qmm_gemm(const qh_qmm_prepared *p, int m, const void *act, void
 qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
 // The persistent int4 decode GEMV for M <= 4; returns QH_STATUS_SHAPE_UNSUPPORTED (without
 // launching or recording an error) for the shapes it does not take.
+// Compute units of the current device (cached per device; 0 if the query fails).
+int device_cu_count();
 qh_status launch_qmm_gemv_unit(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream);
 bool gemv_fits(const qh_qmm_prepared *p, int m);  // the GEMV's LDS staging holds M x K
 qh_status launch_qmm_accumulate(const qh_qmm_prepared *p, int m, const void *act, int64_t *acc,
