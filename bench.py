@@ -355,6 +355,21 @@ def measured_traffic(kernel_key: str):
         return None
 
 
+def vendor_int8_gemm_workload(M: int, K: int, N: int, steps: int, warmup: int):
+    """Context, not a product path: the vendor library's plain int8 GEMM (torch._int_mm, i8 x i8
+    -> i32, no requantisation) at the primary shape on the same GPU, for comparison with the
+    requantising kernel above."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    a = torch.randint(-128, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
+    b = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    bt = b.t()
+    wall, ev = time_kernel(lambda i: torch._int_mm(a, bt), steps, warmup)
+    return {"m": M, "k": K, "n": N, "ms": ev, "wall_ms": wall, "tops": 2.0 * M * K * N / (ev * 1e-3) / 1e12,
+            "what": "torch._int_mm (i8 x i8 -> i32, no requantisation)"}
+
+
 def lpbq_expand_workload(k: int, n: int, steps: int, warmup: int):
     """HmxW4LpbqExpandToI8 on the device: [K/2, N] int4 K-pair codes + [N * K/32] scales -> [K, N]
     int8 K-major tiles.  Byte work: K*N/2 + N*K/32 bytes in, K*N bytes out."""
@@ -420,6 +435,7 @@ def main() -> int:
             jobs.append((f"gdn_prefill_c64_{'fp32' if prec == 0 else 'bf16'}",
                          lambda prec=prec: gdn_prefill_workload(8, 4096, 32, 10, 2, prec)))
         jobs.append(("lpbq_expand_4096x14336", lambda: lpbq_expand_workload(4096, 14336, 20, 3)))
+        jobs.append(("vendor_int8_gemm_4096", lambda: vendor_int8_gemm_workload(M, K, N, 20, 5)))
         for key, job in jobs:
             if args.only and not re.search(args.only, key):
                 continue
