@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
   ChunkIn<WU_F32> in;
   load_chunk<WU_F32>(a, of, 0, in);
 
-  for (int n = 0; n < a.nchunks; ++n) {
+  auto chunk = [&](const int n) __attribute__((always_inline)) {
     // ---- L: q, k, W into LDS; norms; g, e^g, e^{g_last - g} ------------------------------------
     {
       const int row = t >> 3, seg = t & 7;
@@ -257,7 +257,10 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
       for (int e = 0; e < 4; ++e) u[i][e] = in.u[i][e];
     }
     lds_barrier();
-    if (n + 1 < a.nchunks) load_chunk<WU_F32>(a, of, n + 1, in);
+    // Unconditional (the last chunk reloads itself, unused): behind a branch the compiler would
+    // lose count of the loads in flight and make the next chunk wait for every memory operation,
+    // this chunk's o stores included, instead of just these loads.
+    load_chunk<WU_F32>(a, of, min(n + 1, a.nchunks - 1), in);
 
     // ---- M: W S, q^ S, v_new; P tiles ----------------------------------------------------------
     Half4 sB[8];
@@ -367,7 +370,12 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
       }
     }
     lds_barrier();  // the next chunk overwrites q, k, W, P and the decays
-  }
+  };
+  // Chunk 0 runs on its own: then every path into the loop has the same memory operations in
+  // flight (the next chunk's loads, then this chunk's o stores), and the compiler's wait before
+  // the first use of the loads counts only them.
+  chunk(0);
+  for (int n = 1; n < a.nchunks; ++n) chunk(n);
 
 #pragma unroll
   for (int kb = 0; kb < 8; ++kb) {
