@@ -138,6 +138,28 @@ def gemv_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     return res
 
 
+def stream_copy_workload(nbytes: int, steps: int, copies: int):
+    """Context, not a product path: the vendor's elementwise copy (torch copy_, nbytes / 2 read and
+    nbytes / 2 written: the GEMV's byte count in total), timed like the GEMV (a replayed graph of
+    back-to-back launches over rotated sources): what a kernel that moves this many bytes once
+    costs on this GPU, launch gaps included."""
+    import torch
+
+    n = nbytes // 8  # int32 elements per direction
+    srcs = [torch.randint(0, 1 << 20, (n,), dtype=torch.int32, device="cuda") for _ in range(copies)]
+    dst = torch.empty((n,), dtype=torch.int32, device="cuda")
+    dst.copy_(srcs[0])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            dst.copy_(srcs[i % copies])
+    wall, ev = time_kernel(lambda i: graph.replay(), 3, 1)
+    ev /= steps
+    return {"bytes": 8 * n, "ms": ev, "wall_ms": wall / steps, "gbs": 8 * n / (ev * 1e-3) / 1e9, "copies": copies,
+            "what": "torch copy_ of int32 (half the bytes read, half written), graph-replayed over rotated sources"}
+
+
 def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
     import numpy as np
     import torch
@@ -436,6 +458,7 @@ def main() -> int:
                          lambda prec=prec: gdn_prefill_workload(8, 4096, 32, 10, 2, prec)))
         jobs.append(("lpbq_expand_4096x14336", lambda: lpbq_expand_workload(4096, 14336, 20, 3)))
         jobs.append(("vendor_int8_gemm_4096", lambda: vendor_int8_gemm_workload(M, K, N, 20, 5)))
+        jobs.append(("vendor_copy_gemv_bytes", lambda: stream_copy_workload(30_410_000, 200, 10)))
         for key, job in jobs:
             if args.only and not re.search(args.only, key):
                 continue
