@@ -41,7 +41,12 @@ constexpr int kThreads = 512;   // 8 waves
 constexpr int kQs = kD + 8;     // LDS row stride of the q / k stores, bf16 (16-byte aligned rows)
 constexpr int kRs = kD + 4;     // LDS row stride of the W store, words
 constexpr int kPs = kC + 4;     // LDS row stride of P, words
-constexpr int kTs = kC + 4;     // LDS row stride of k^T, bf16 (8-byte aligned rows)
+// k^T in LDS: row stride 72 bf16 = 36 words (= 4 mod 8: the 8-byte fragment reads of 16 keys x
+// 4 lane quarters are conflict-free), and the 4-token groups of key kappa stored at group
+// (t / 4) ^ (2 (kappa / 16)), so the transposing 2-byte writes of one instruction (8 key segments
+// of 16) land in 8 distinct 4-word windows instead of two.
+constexpr int kTs = kC + 8;
+__device__ __forceinline__ int kt_col(int key, int tok) { return 4 * ((tok >> 2) ^ (2 * (key >> 4))) + (tok & 3); }
 
 struct StateArgs {
   const uint16_t *q, *k;  // bf16 [B][T][H][D]
@@ -204,10 +209,11 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
       *reinterpret_cast<uint4 *>(&Kl[row][16 * seg + 8]) = in.k[1];
       {
         const uint32_t kw[8] = {in.k[0].x, in.k[0].y, in.k[0].z, in.k[0].w, in.k[1].x, in.k[1].y, in.k[1].z, in.k[1].w};
+        const int col = kt_col(16 * seg, row);
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-          KlT[16 * seg + 2 * x][row] = static_cast<uint16_t>(kw[x] & 0xFFFFu);
-          KlT[16 * seg + 2 * x + 1][row] = static_cast<uint16_t>(kw[x] >> 16);
+          KlT[16 * seg + 2 * x][col] = static_cast<uint16_t>(kw[x] & 0xFFFFu);
+          KlT[16 * seg + 2 * x + 1][col] = static_cast<uint16_t>(kw[x] >> 16);
         }
       }
       float f[16];
@@ -366,7 +372,8 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb) {
         const uint16_t *krow = KlT[16 * kb + r16];  // key 16 kb + r16 = row of k^T
-        S[kb] = mma_exact_a<SPLIT>(bf16x4(krow + c), bf16x4(krow + c + 16), dB[2 * p], dB[2 * p + 1], S[kb]);
+        S[kb] = mma_exact_a<SPLIT>(bf16x4(krow + kt_col(16 * kb, c)), bf16x4(krow + kt_col(16 * kb, c + 16)), dB[2 * p],
+                                   dB[2 * p + 1], S[kb]);
       }
     }
     lds_barrier();  // the next chunk overwrites q, k, W, P and the decays
