@@ -297,26 +297,22 @@ __device__ __forceinline__ void solve_head(const GdnArgs &g, uint32_t (*Tl)[kTs]
     tile_task<1>(wave, b1, i1);
     load_tile<U16, 1>(g, hbase, b1, i1, task, lane, a1);
   }
-  if (P > 64) {
-    tile_task<2>(wave, b2, i2);
-    load_tile<U16, 2>(g, hbase, b2, i2, task, lane, a2);
-  }
-  if (P > 128) {
-    tile_task<4>(wave, b4, i4);
-    load_tile<U16, 4>(g, hbase, b4, i4, task, lane, a4);
-  }
+  if (P > 64) tile_task<2>(wave, b2, i2);
+  if (P > 128) tile_task<4>(wave, b4, i4);
   // last merge, strip `part`, tile `wave`: k blocks l = part + 2 p + h
   constexpr int kPF = (NBF + 1) / 2;
   float4 af[kPF][2];
+  auto load_last = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int p = 0; p < kPF; ++p) {
+    for (int p = 0; p < kPF; ++p) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int l = part + 2 * p + h;
-      af[p][h] = load_a4_or0<U16>(g, hbase, P / 2 + 16 * wave + r16, 16 * l + 4 * q,
-                                  wave < NBF && l < NBF && P / 2 + 16 * wave < C && 16 * l < C);
+      for (int h = 0; h < 2; ++h) {
+        const int l = part + 2 * p + h;
+        af[p][h] = load_a4_or0<U16>(g, hbase, P / 2 + 16 * wave + r16, 16 * l + 4 * q,
+                                    wave < NBF && l < NBF && P / 2 + 16 * wave < C && 16 * l < C);
+      }
     }
-  }
+  };
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- level 0 ------------------------------------------------------------------------------------
@@ -331,8 +327,15 @@ __device__ __forceinline__ void solve_head(const GdnArgs &g, uint32_t (*Tl)[kTs]
   store_zeros<U16>(g, hbase, part, wave, lane);
 
   // ---- merges inside the halves -------------------------------------------------------------------
+  // Each level's A tiles are requested one level ahead (the last merge's strip two ahead), so the
+  // requests are issued a few at a time; the stores issued before them are a level old by the
+  // time the wait for them (which counts those stores too) comes.
+  if (P > 64) load_tile<U16, 2>(g, hbase, b2, i2, task, lane, a2);
+  if (P <= 128) load_last();
   if (P > 32) merge_level<U16, SPLIT, 1>(g, hbase, Tl, task, owner, b1, i1, a1, lane);
+  if (P > 128) load_tile<U16, 4>(g, hbase, b4, i4, task, lane, a4);
   if (P > 64) merge_level<U16, SPLIT, 2>(g, hbase, Tl, task, owner, b2, i2, a2, lane);
+  if (P > 128) load_last();
   if (P > 128) merge_level<U16, SPLIT, 4>(g, hbase, Tl, task, owner, b4, i4, a4, lane);
 
   // ---- last merge, strip `part`: Y tiles (one per wave) through LDS, then T21 = T22 Y -----------
