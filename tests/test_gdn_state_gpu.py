@@ -76,16 +76,19 @@ def stage_a_exact(kb, vb, beta, gc):
 
 @pytest.mark.parametrize("precision", [0, 1], ids=["fp32", "bf16"])
 @pytest.mark.parametrize("with_state", [False, True], ids=["zero_state", "incoming_state"])
-def test_chunk_state_matches_fp64(gpu, precision, with_state):
+@pytest.mark.parametrize("T", [192, 64], ids=["three_chunks", "one_chunk"])
+def test_chunk_state_matches_fp64(gpu, precision, with_state, T):
+    """Stage B against the float64 recurrence; one chunk runs only the first (peeled) chunk, whose
+    next-chunk prefetch reloads itself."""
     import torch
 
     from qcom_htp_amd.gdn import gdn_chunk_state
 
-    B, T, H = 2, 192, 3
+    B, H = 2, 3
     qb, kb, vb, beta, gc = seq_inputs(B, T, H, seed=21 + with_state)
     W, U = stage_a_exact(kb, vb, beta, gc)
     S0 = (np.random.default_rng(5).standard_normal((B, H, 128, 128)) * 0.05).astype(np.float32) if with_state else None
-    print(f"[gdn-state] stage B precision={precision} state={with_state}", flush=True)
+    print(f"[gdn-state] stage B T={T} precision={precision} state={with_state}", flush=True)
     o, S = gdn_chunk_state(to_dev(qb, gpu), to_dev(kb, gpu), to_dev(gc, gpu), to_dev(W.astype(np.float32), gpu),
                            to_dev(U.astype(np.float32), gpu), None if S0 is None else to_dev(S0, gpu),
                            precision=precision, out_dtype=torch.float32)
