@@ -23,6 +23,7 @@
 
 #include <atomic>
 
+#include "lane_ops.h"
 #include "qmm_internal.h"
 
 namespace qh {
@@ -167,11 +168,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
   auto phase1 = [&]() __attribute__((always_inline)) {
     float gv = t < C ? gpre : 0.0f;
     if (t < C) bs[t] = bpre;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(gv, off, 64);
-      if (lane >= off) gv += y;
-    }
+    gv = scan64(gv);  // DPP: no LDS round trips
     if (lane == 63 && wave < 4) wsum[wave] = gv;
 #pragma unroll
     for (int p = 0; p < kRowPasses; ++p) {
@@ -187,9 +184,7 @@ __device__ __forceinline__ void chunk_items(const ChunkArgs &a, const int nitems
         ss = fmaf(f[2 * i], f[2 * i], ss);
         ss = fmaf(f[2 * i + 1], f[2 * i + 1], ss);
       }
-      ss += __shfl_xor(ss, 1, 64);
-      ss += __shfl_xor(ss, 2, 64);
-      ss += __shfl_xor(ss, 4, 64);
+      ss = sum8(ss);
       const float inv = rsqrtf(ss + 1e-6f);
       if (part == 0) rn[row] = inv;
       uint32_t o[8];
