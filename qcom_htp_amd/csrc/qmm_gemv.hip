@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kGemvThreads = 256;
 constexpr int kGemvWaves = kGemvThreads / 64;
-constexpr int kGemvMaxDynLds = 140 * 1024;  // activation planes + k-group sums (+ <= 17 KB static)
+constexpr int kGemvMaxDynLds = 139 * 1024;  // activation planes + k-group sums (+ <= 21 KB static)
 constexpr int kU = kGemvKU;                  // k-groups per lane per batch (loads in flight)
 
 struct GemvArgs {
@@ -260,6 +260,9 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   __shared__ int red[kGemvWaves][MM][16];
   __shared__ int red2[A16 ? kGemvWaves : 1][A16 ? MM : 1][16];
   __shared__ int red3[HR ? kGemvWaves : 1][HR ? MM : 1][16];
+  // 16 rows (matrix core) also form sum_k lo'_k r_k, so their dot products are exact
+  constexpr bool LR = HR && MM == 16;
+  __shared__ int red4[LR ? kGemvWaves : 1][LR ? MM : 1][16];
   __shared__ uint4 rtab[HR ? 16 * kRtabF : 1];  // [column][block scale f = 0 .. 16]
   __shared__ uint32_t r1[16];
   __shared__ uint16_t fix_list[MM * 16];
@@ -359,7 +362,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
       if (A16 && !kMfma) acc2[m] = 0;
       if (HR && !kMfma) acc3[m] = 0;
     }
-    v4i macc = {0, 0, 0, 0}, macc2 = {0, 0, 0, 0}, macc3 = {0, 0, 0, 0};
+    v4i macc = {0, 0, 0, 0}, macc2 = {0, 0, 0, 0}, macc3 = {0, 0, 0, 0}, macc4 = {0, 0, 0, 0};
     for (int i0 = 0; i0 < iters; i0 += kU) {
       if (i0 > 0) issue(grp, i0);
       if constexpr (kMfma) {
@@ -415,6 +418,8 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
             for (int j = 0; j < 4; ++j) {
               const uint2 a = al[j];
               macc2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(b[2 * j], b[2 * j + 1]), macc2, 0, 0, 0);
+              if constexpr (LR)
+                macc4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(rr[2 * j], rr[2 * j + 1]), macc4, 0, 0, 0);
             }
           }
         }
@@ -483,6 +488,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         red[wave][4 * sub + q][col] = macc[q];
         if (A16) red2[wave][4 * sub + q][col] = macc2[q];
         if (HR) red3[wave][4 * sub + q][col] = macc3[q];
+        if (LR) red4[wave][4 * sub + q][col] = macc4[q];
       }
     }
 #pragma unroll
@@ -506,24 +512,26 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     const int om = t >> 4, n = grp * 16 + (t & 15);
     bool amb = false;
     if (owns_out) {
-      int S1 = 0, S2 = 0, S3 = 0;
+      int S1 = 0, S2 = 0, S3 = 0, S4 = 0;
 #pragma unroll
       for (int w = 0; w < kGemvWaves; ++w) {
         S1 += red[w][om][t & 15];
         if (A16) S2 += red2[w][om][t & 15];
         if (HR) S3 += red3[w][om][t & 15];
+        if (LR) S4 += red4[w][om][t & 15];
       }
       const double beta = ep.beta, margin = ep.margin, absb = ep.absb, mr1 = ep.mr1;
       const int64_t corr = A16 ? ep.corr * static_cast<int64_t>(128 + 32768 - g.act_zp) : ep.corr;
       const int64_t S = A16 ? 256 * static_cast<int64_t>(S1) + S2 + corr : static_cast<int64_t>(S1) + corr;
       double tv, slack;
       if constexpr (HR) {
-        // D = sum_k (a - zp) (w M + r) but for sum_k lo'_k r_k, bounded by mr1:
-        //   M S + 256 sum hi' r + (32896 - zp) sum r
-        const int64_t D = S * ep.mant + 256 * static_cast<int64_t>(S3) +
+        // D = sum_k (a - zp) (w M + r) = M S + 256 sum hi' r + sum lo' r + (32896 - zp) sum r.
+        // 16 rows form sum lo' r too (D exact: only the oracle's own float noise remains);
+        // fewer rows bound it by mr1 (margin_lo).
+        const int64_t D = S * ep.mant + 256 * static_cast<int64_t>(S3) + static_cast<int64_t>(S4) +
                           static_cast<int64_t>(128 + 32768 - g.act_zp) * ep.csr;
         tv = fma(static_cast<double>(D), ep.alpha, beta);
-        slack = margin + mr1 + 0x1p-48 * (fabs(tv) + absb);
+        slack = margin + (LR ? 0.0 : mr1) + 0x1p-48 * (fabs(tv) + absb);
       } else {
         const double alpha = A16 ? ep.alpha * static_cast<double>(ep.mant) : ep.alpha;
         tv = fma(static_cast<double>(S), alpha, beta);
