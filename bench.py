@@ -99,6 +99,34 @@ def gemm_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     return res, case
 
 
+def gemm_rotated_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, copies: int):
+    """The GEMM over `copies` prepared weight sets and activation buffers in turn (more bytes
+    than the 256 MB MALL holds), so every launch reads its operands from HBM; every copy's
+    output is checked against the oracle after the timed region."""
+    import torch
+
+    from qcom_htp_amd import cases
+    from qcom_htp_amd.qmm import PATH_GEMM, QuantMatmul
+
+    dev = torch.device("cuda", 0)
+    case = cases.synthetic_case(family, m, k, n, seed=2)
+    ops = [QuantMatmul.from_case(case, device=dev) for _ in range(copies)]
+    act0 = torch.from_numpy(case.activation_q).to(dev)
+    acts = [act0.clone() for _ in range(copies)]
+    outs = [torch.empty((m, n), dtype=ops[0].out_dtype, device=dev) for _ in range(copies)]
+    wall, ev = time_kernel(lambda i: ops[i % copies](acts[i % copies], out=outs[i % copies], path=PATH_GEMM), steps, warmup)
+    torch.cuda.synchronize()
+    res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "tops": 2.0 * m * k * n / (ev * 1e-3) / 1e12,
+           "copies": copies, "rotated_mb": copies * (k * n + m * k) / 1e6}  # int8 weight tiles + activations
+    res.update(parity_check(case, outs[0].cpu().numpy()))
+    same = all(torch.equal(outs[0], o) for o in outs[1:])
+    if not same:
+        raise RuntimeError("rotated GEMM copies disagree")
+    for op in ops:
+        op.close()
+    return res
+
+
 def gemv_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, copies: int, lpbq_block: int = 64):
     import torch
 
@@ -444,6 +472,7 @@ def main() -> int:
         jobs = []
         for fam in ("w8a16", "u8i8", "w4a16_per_channel"):
             jobs.append((f"{fam}_gemm_4096", lambda fam=fam: gemm_workload(fam, M, K, N, max(5, args.steps // 2), 2)[0]))
+        jobs.append(("w4a8_gemm_4096_rotated", lambda: gemm_rotated_workload("w4a8_per_channel", M, K, N, 20, 10, copies=10)))
         for fam in ("w4a8_lpbq", "w4a16_lpbq"):
             jobs.append((f"{fam}_gemm_4096x14336", lambda fam=fam: gemm_workload(fam, 4096, 4096, 14336, 5, 2)[0]))
         for fam in ("w4a8_lpbq", "w4a16_lpbq"):
