@@ -18,8 +18,9 @@
 // merge (T21 rows P/2 .. P-1).  The G workgroups of a head get block indexes of one residue mod
 // 8, which places them on one XCD and one L2.
 // Inside the halves a level gives each wave one 16-row tile of one merge's T21:
-//   Y[i][:] = A21[i][:] T11 (written to LDS transposed, in the T21 region), then
-//   X[i][:] = sum_{l <= i} T22[i][l] Y[l][:]  (registers; stored after every wave has read Y).
+//   Y[i][:] = A21[i][:] T11, written to LDS transposed in the merge's upper-right block (the
+//            zero block T12, which no product ever reads), then
+//   X[i][:] = sum_{l <= i} T22[i][l] Y[l][:]  (registers; into the T21 region at once).
 // The products run on v_mfma_f32_16x16x32_bf16: a 32-deep k step takes rows 4q .. 4q+3 of two
 // 16-row blocks, the k order in which the MFMA result layout (lane: rows 4q .. 4q+3 of one
 // column) is read back as the next B operand.
@@ -129,8 +130,9 @@ __device__ __forceinline__ void load_tile(const GdnArgs &g, size_t hbase, int b,
 }
 
 // One merge level inside the halves (NB tiles per block), tile i of the merge at row b per task
-// wave; `owner` marks the workgroup that stores this task's T21 tile.  Three barriers: Y into
-// the T21 region, X from Y, X into the T21 region.
+// wave; `owner` marks the workgroup that stores this task's T21 tile.  Two barriers: Y complete
+// (in the upper-right block, rows b .. b + s, columns b + s .. b + 2 s), then X complete (in the
+// T21 region, which no wave reads during the X products).
 template <bool U16, bool SPLIT, int NB>
 __device__ __forceinline__ void merge_level(const GdnArgs &g, size_t hbase, uint32_t (*Tl)[kTs], bool task, bool owner,
                                             int b, int i, const float4 (&av)[NB], int lane) {
@@ -154,8 +156,9 @@ __device__ __forceinline__ void merge_level(const GdnArgs &g, size_t hbase, uint
         const Half4 t1 = two ? unpack4(Tl[r0 + 16][c], Tl[r0 + 17][c], Tl[r0 + 18][c], Tl[r0 + 19][c]) : kZero4;
         acc = mma<SPLIT>(as[l], two ? as[l + 1] : kZero4, t0, t1, acc);
       }
-      // Y tile (i, j) transposed in place of T21 tile (i, j): row rt + column, column c0 + row
-      *reinterpret_cast<uint4 *>(&Tl[rt + r16][b - shift + 16 * j + 4 * q]) =
+      // Y tile (i, j) transposed at tile (i, j) of the upper-right block: row b + 16 i + column,
+      // column b + s + 16 j + row (half-local)
+      *reinterpret_cast<uint4 *>(&Tl[b + 16 * i + r16][b - shift + s + 16 * j + 4 * q]) =
           make_uint4(hilo<SPLIT>(acc[0]), hilo<SPLIT>(acc[1]), hilo<SPLIT>(acc[2]), hilo<SPLIT>(acc[3]));
     }
   }
@@ -170,10 +173,10 @@ __device__ __forceinline__ void merge_level(const GdnArgs &g, size_t hbase, uint
       const int cA = b + s - shift + 16 * l + 4 * q;  // Tl column of T22's block l, this lane's k
       const Half4 w0 = unpack4(*reinterpret_cast<const uint4 *>(trow + cA));
       const Half4 w1 = two ? unpack4(*reinterpret_cast<const uint4 *>(trow + cA + 16)) : kZero4;
-      const uint32_t *yrow = Tl[b + s + 16 * l + r16];  // transposed Y tile (l, j): column r16 of it
+      const uint32_t *yrow = Tl[b + 16 * l + r16];  // transposed Y tile (l, j): column r16 of it
 #pragma unroll
       for (int j = 0; j < NB; ++j) {
-        const int c = b - shift + 16 * j + 4 * q;
+        const int c = b - shift + s + 16 * j + 4 * q;
         const Half4 y0 = unpack4(*reinterpret_cast<const uint4 *>(yrow + c));
         const Half4 y1 = two ? unpack4(*reinterpret_cast<const uint4 *>(yrow + 16 * kTs + c)) : kZero4;
         X[j] = mma<SPLIT>(w0, w1, y0, y1, X[j]);
@@ -184,9 +187,6 @@ __device__ __forceinline__ void merge_level(const GdnArgs &g, size_t hbase, uint
       for (int j = 0; j < NB; ++j)
         if (b + 16 * j < g.C) store_tile<U16>(g, hbase, rt, b + 16 * j + r16, q, X[j]);
     }
-  }
-  lds_barrier();
-  if (task) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
 #pragma unroll
