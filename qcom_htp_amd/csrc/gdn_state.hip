@@ -42,12 +42,6 @@ constexpr int kThreads = 512;   // 8 waves
 constexpr int kQs = kD + 8;     // LDS row stride of the q / k stores, bf16 (16-byte aligned rows)
 constexpr int kRs = kD + 4;     // LDS row stride of the W store, words
 constexpr int kPs = kC + 4;     // LDS row stride of P, words
-// k^T in LDS: row stride 72 bf16 = 36 words (= 4 mod 8: the 8-byte fragment reads of 16 keys x
-// 4 lane quarters are conflict-free), and the 4-token groups of key kappa stored at group
-// (t / 4) ^ (2 (kappa / 16)), so the transposing 2-byte writes of one instruction (8 key segments
-// of 16) land in 8 distinct 4-word windows instead of two.
-constexpr int kTs = kC + 8;
-__device__ __forceinline__ int kt_col(int key, int tok) { return 4 * ((tok >> 2) ^ (2 * (key >> 4))) + (tok & 3); }
 
 struct StateArgs {
   const uint16_t *q, *k;  // bf16 [B][T][H][D]
@@ -141,13 +135,23 @@ __device__ __forceinline__ Half4 bf16x4(const uint16_t *p) {
   const uint2 v = *reinterpret_cast<const uint2 *>(p);
   return exact4(v.x, v.y);
 }
+
+// 4 bf16 of one column of a row-major LDS tile, by a transposing LDS read (ds_read_b64_tr_b16):
+// in each group of 16 lanes, lane j receives element j % 4 of the 8 bytes addressed by lane
+// 4 e + j / 4 as its element e.  So if lane 4 e + a of the group addresses row r0 + e, columns
+// c0 + 4 a .. + 3, lane j receives rows r0 .. r0 + 3 of column c0 + j.
+__device__ __forceinline__ Half4 bf16x4_tr(const uint16_t *p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(p));
+  const uint2 v = __builtin_bit_cast(uint2, r);
+  return exact4(v.x, v.y);
+}
 template <bool SPLIT, bool WU_F32, bool OUT_F32>
 __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
   // q, k rows as given (bf16, exact MFMA operands) with their l2norm factors; W as hi | lo words;
   // P as hi | lo words (lower tiles); g, e^g, e^{g_last - g} per token
   __shared__ __attribute__((aligned(16))) uint16_t Ql[kC][kQs];
   __shared__ __attribute__((aligned(16))) uint16_t Kl[kC][kQs];
-  __shared__ __attribute__((aligned(16))) uint16_t KlT[kD][kTs];  // k transposed: key, token
   __shared__ __attribute__((aligned(16))) uint32_t Wl[kC][kRs];
   __shared__ __attribute__((aligned(16))) uint32_t Pl[kC][kPs];
   __shared__ float invq[kC], invk[kC];  // 1 / |q| / sqrt(D), 1 / |k| (eps 1e-6 inside the root)
@@ -180,15 +184,6 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
       *reinterpret_cast<uint4 *>(&Ql[row][16 * seg + 8]) = in.q[1];
       *reinterpret_cast<uint4 *>(&Kl[row][16 * seg]) = in.k[0];
       *reinterpret_cast<uint4 *>(&Kl[row][16 * seg + 8]) = in.k[1];
-      {
-        const uint32_t kw[8] = {in.k[0].x, in.k[0].y, in.k[0].z, in.k[0].w, in.k[1].x, in.k[1].y, in.k[1].z, in.k[1].w};
-        const int col = kt_col(16 * seg, row);
-#pragma unroll
-        for (int x = 0; x < 8; ++x) {
-          KlT[16 * seg + 2 * x][col] = static_cast<uint16_t>(kw[x] & 0xFFFFu);
-          KlT[16 * seg + 2 * x + 1][col] = static_cast<uint16_t>(kw[x] >> 16);
-        }
-      }
       float f[16];
       unbf16x8(in.q[0], f);
       unbf16x8(in.q[1], f + 8);
@@ -339,14 +334,17 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) S[kb][e] *= el;
     }
+    // k^T operand (key 16 kb + r16, tokens c .. c + 3 and c + 16 .. c + 19) read from the
+    // row-major k tile by transposing reads: lane 4 e + a of each 16-lane group addresses token
+    // c + e, keys 16 kb + 4 a .. + 3
+    const int te = r16 >> 2, ka = r16 & 3;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {  // token blocks 2p, 2p + 1: 8 independent accumulations
       const int c = 32 * p + 4 * qd;
 #pragma unroll
       for (int kb = 0; kb < 8; ++kb) {
-        const uint16_t *krow = KlT[16 * kb + r16];  // key 16 kb + r16 = row of k^T
-        S[kb] = mma_exact_a<SPLIT>(bf16x4(krow + kt_col(16 * kb, c)), bf16x4(krow + kt_col(16 * kb, c + 16)), dB[2 * p],
-                                   dB[2 * p + 1], S[kb]);
+        S[kb] = mma_exact_a<SPLIT>(bf16x4_tr(&Kl[c + te][16 * kb + 4 * ka]), bf16x4_tr(&Kl[c + 16 + te][16 * kb + 4 * ka]),
+                                   dB[2 * p], dB[2 * p + 1], S[kb]);
       }
     }
     lds_barrier();  // the next chunk overwrites q, k, W, P and the decays
