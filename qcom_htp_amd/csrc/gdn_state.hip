@@ -14,13 +14,14 @@
 // bf16_split.h), so W S and q S take S straight from the accumulators.  q and k stay the bf16
 // values they arrive as (exact MFMA operands); their l2norm factors scale the products' rows and
 // columns instead.  Per chunk:
-//   L. q, k rows, k transposed and W (bf16 hi | lo words) into LDS; the row norms (8-lane DPP
+//   L. q, k rows and W (bf16 hi | lo words) into LDS; the row norms (8-lane DPP
 //      sums); g's prefix sum (64-lane DPP scan), e^g and e^{g_last - g} by one wave;
 //   M. each wave: W S and q S for its 16 value columns (4 token tiles), v_new = U - W S with U
 //      from registers, o's first term e^g q^ S; the 10 lower 16 x 16 tiles of q k^T over the
 //      waves, scaled by the norms and decays, into LDS as P;
 //   O. o = e^g q^ S + P v_new for the wave's columns (causal tiles only), stored;
-//   S. S = e^{g_last} S + k^T ((e^{g_last - g} / |k|) v_new), k^T from its transposed copy.
+//   S. S = e^{g_last} S + k^T ((e^{g_last - g} / |k|) v_new), k^T read from the k rows by LDS
+//      transpose reads.
 // The next chunk's q, k, W, U and gc are read into registers during M, so their latency
 // overlaps this chunk's products; the workgroup issues them before its stores of o.
 // Precision: QH_GDN_FP32 carries W, S, P and v_new as bf16 hi/lo splits (hi*hi + hi*lo + lo*hi,
