@@ -306,14 +306,28 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
                          two ? unpack4(*reinterpret_cast<const uint4 *>(prow + c + 16)) : kZero4, vB[2 * p],
                          two ? vB[2 * p + 1] : kZero4, acc);
       }
+      if constexpr (OUT_F32) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t oi = of.tile + static_cast<uint32_t>(n * kC + 16 * i + e) * of.tok;
-        if (OUT_F32) {
-          static_cast<float *>(a.o)[oi] = acc[e];
-        } else {
-          static_cast<uint16_t *>(a.o)[oi] = static_cast<uint16_t>(pack_bf16(acc[e], 0.0f) & 0xFFFFu);
-        }
+        for (int e = 0; e < 4; ++e)
+          static_cast<float *>(a.o)[of.tile + static_cast<uint32_t>(n * kC + 16 * i + e) * of.tok] = acc[e];
+      } else {
+        // the quad's 4 rows x 4 adjacent columns, transposed with DPP quad broadcasts so that lane
+        // q of the quad stores row 4 qd + q, the quad's 4 columns, in one 8-byte store
+        const int qq = r16 & 3;
+        const uint32_t P0 = pack_bf16(acc[0], acc[1]), P1 = pack_bf16(acc[2], acc[3]);
+        const uint32_t a0 = __builtin_amdgcn_mov_dpp(P0, 0x00, 0xF, 0xF, false);
+        const uint32_t a1 = __builtin_amdgcn_mov_dpp(P0, 0x55, 0xF, 0xF, false);
+        const uint32_t a2 = __builtin_amdgcn_mov_dpp(P0, 0xAA, 0xF, 0xF, false);
+        const uint32_t a3 = __builtin_amdgcn_mov_dpp(P0, 0xFF, 0xF, 0xF, false);
+        const uint32_t b0 = __builtin_amdgcn_mov_dpp(P1, 0x00, 0xF, 0xF, false);
+        const uint32_t b1 = __builtin_amdgcn_mov_dpp(P1, 0x55, 0xF, 0xF, false);
+        const uint32_t b2 = __builtin_amdgcn_mov_dpp(P1, 0xAA, 0xF, 0xF, false);
+        const uint32_t b3 = __builtin_amdgcn_mov_dpp(P1, 0xFF, 0xF, 0xF, false);
+        const uint32_t sel = (qq & 1) ? 0x07060302u : 0x05040100u;
+        const uint2 w = qq < 2 ? make_uint2(__builtin_amdgcn_perm(a1, a0, sel), __builtin_amdgcn_perm(a3, a2, sel))
+                               : make_uint2(__builtin_amdgcn_perm(b1, b0, sel), __builtin_amdgcn_perm(b3, b2, sel));
+        const uint32_t oi = of.tile - static_cast<uint32_t>(qq) + static_cast<uint32_t>(n * kC + 16 * i + qq) * of.tok;
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.o) + oi) = w;
       }
     }
 

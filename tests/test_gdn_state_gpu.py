@@ -151,6 +151,28 @@ def test_state_handoff_equals_one_pass(gpu):
     assert torch.equal(S2, S_all)
 
 
+@pytest.mark.parametrize("precision", [0, 1], ids=["fp32", "bf16"])
+def test_chunk_state_bf16_output_is_rounded_fp32_output(gpu, precision):
+    """The bfloat16 output path (4 rows x 4 columns of each lane quad exchanged so that every lane
+    stores 4 adjacent outputs of one row) gives the float32 output rounded to nearest even, element
+    for element: the two kernels differ only in how o is stored."""
+    import torch
+
+    from qcom_htp_amd.gdn import gdn_chunk_state, gdn_chunk_uw
+
+    B, T, H = 2, 192, 3
+    qb, kb, vb, beta, gc = seq_inputs(B, T, H, seed=43)
+    q, k, v, g, bt = (to_dev(x, gpu) for x in (qb, kb, vb, gc, beta))
+    w, u = gdn_chunk_uw(k, v, g, bt, 64, decay_w=True, out_dtype=torch.float32)
+    print(f"[gdn-state] bf16 output, precision={precision}", flush=True)
+    o32, S32 = gdn_chunk_state(q, k, g, w, u, precision=precision, out_dtype=torch.float32)
+    o16, S16 = gdn_chunk_state(q, k, g, w, u, precision=precision, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert o16.dtype == torch.bfloat16 and o16.shape == o32.shape
+    assert torch.equal(o16, o32.to(torch.bfloat16))
+    assert torch.equal(S16, S32)
+
+
 def test_chunk_state_rejects_bad_arguments(gpu):
     import torch
 
