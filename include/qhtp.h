@@ -12,9 +12,12 @@
  *   - Every entry point validates its arguments and returns a status; no entry point
  *     returns QH_STATUS_OK for a shape it did not compute.  qh_last_error() gives a
  *     human-readable reason for the last failure on the calling thread.
- *   - No global mutable state is shared between calls except the per-thread error text;
- *     prepared handles are read-only during runs, so concurrent runs on different
- *     streams are safe.
+ *   - Prepared handles are read-only during runs, so concurrent runs on different streams
+ *     or host threads are safe, with one exception: qh_qmm_run_chain_noalloc keeps its
+ *     intermediate results in one static array per device, so its calls that overlap on
+ *     one device race and must be serialised by the caller.  Besides that array, the
+ *     library holds only the per-thread error text and per-device caches of device
+ *     attributes (atomic, set once per device).
  */
 #ifndef QHTP_H_
 #define QHTP_H_

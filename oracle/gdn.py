@@ -301,6 +301,31 @@ def chunk_stage_a_torch(k, v, gc, beta, decay_w: bool = True):
     return U, W
 
 
+def chunk_stage_a_solve_torch(k, v, gc, beta, decay_w: bool = True):
+    """The outputs (U, W) of ``chunk_stage_a_torch`` by a batched float64 triangular solve
+    (I - A) [U | W] = [v_beta | k_beta (e^g)] in place of the row recurrence (LAPACK's unit-lower
+    solve; T is never formed).  Same definitions as scripts/gdn_ref_kernel.py:71-89; this form
+    checks every item of a full-size launch in seconds."""
+    import torch
+
+    k = torch.as_tensor(k, dtype=torch.float64)
+    v = torch.as_tensor(v, dtype=torch.float64)
+    gc = torch.as_tensor(gc, dtype=torch.float64)
+    beta = torch.as_tensor(beta, dtype=torch.float64)
+    C = k.shape[-2]
+    kn = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    v_beta = v * beta.unsqueeze(-1)
+    k_beta = kn * beta.unsqueeze(-1)
+    g = torch.cumsum(gc, dim=-1)
+    lower = torch.tril(torch.ones(C, C, dtype=torch.bool), -1)
+    decay = torch.exp(torch.where(lower, g.unsqueeze(-1) - g.unsqueeze(-2), torch.zeros((), dtype=torch.float64)))
+    A = -(k_beta @ kn.transpose(-1, -2)) * decay * lower
+    M = torch.eye(C, dtype=torch.float64) - A
+    rhs = torch.cat([v_beta, k_beta * torch.exp(g).unsqueeze(-1) if decay_w else k_beta], dim=-1)
+    X = torch.linalg.solve_triangular(M, rhs, upper=False, unitriangular=True)
+    return X[..., : v.shape[-1]], X[..., v.shape[-1]:]
+
+
 def _l2n(x):
     import torch
 

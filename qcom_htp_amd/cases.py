@@ -44,6 +44,14 @@ __all__ = [
     "quantize_weight",
     "make_case",
     "synthetic_case",
+    "uniform_u8i8_case",
+    "GraphCase",
+    "GRAPH_FAMILIES",
+    "W4A16_PRECISION_SUITE",
+    "graph_activation",
+    "graph_weight_kn",
+    "graph_lpbq_block_scales",
+    "graph_case",
 ]
 
 
@@ -475,3 +483,158 @@ def synthetic_case(
         lpbq_expanded_q_nk=expanded,
         seed=seed,
     )
+
+
+def uniform_u8i8_case(m: int = 256, k: int = 256, n: int = 256, seed: int = 1) -> QmmCase:
+    """The u8i8 matmul described with fixed per-tensor parameters instead of min/max-derived ones:
+
+    * activations uint8 ~ U[0, 255], scale 0.02, offset -128 (zero point 128);
+    * weights int8 ~ U[-127, 127], one scale 0.01 for every output channel;
+    * int32 bias ~ U[-2^15, 2^15] at the bias scale 0.02 * 0.01;
+    * output uint8, scale 0.05, offset 0.
+
+    The seven seeded cases of ``make_case`` derive their scales from each case's float ranges;
+    this one keeps the stated constants, so most outputs land on the clip rails.
+    """
+    fam = FAMILIES["u8i8"]
+    rng = np.random.default_rng(seed)
+    x_q = rng.integers(0, 256, size=(m, k)).astype(np.uint8)
+    q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+    s32 = np.full(n, 0.01, dtype=np.float32)
+    bias_q = rng.integers(-(1 << 15), (1 << 15) + 1, size=n).astype(np.int32)
+    deq = q.astype(np.float32) * s32[:, None]
+    return QmmCase(family=fam, case="uniform_fixed_scales", m=m, k=k, n=n, activation_q=x_q, weight_q_nk=q,
+                   weight_scale=s32, bias_q=bias_q, act_scale=0.02, out_scale=0.05, weight_deq=deq, seed=seed)
+
+
+# ---------------------------------------------------------------------------- graph operands
+# The reference's CHAIN graphs (its op-package perf and CI flows) do not use the seeded float
+# cases above: their operands are closed-form integer patterns, and their expected outputs are
+# integer contracts applied chain times (gen_quant_chain.py:1525-1560).  The restatements below
+# produce the same operands; the contracts run through qh_qmm_run_contract.
+
+GRAPH_SEED_STRIDE = 374761393  # activation seed = (index + 1) * this (gen_quant_chain.py:271)
+
+
+def graph_activation(act_bits: int, m: int, k: int, index: int = 0, mode: str = "default",
+                     impulse_k: int = 0) -> np.ndarray:
+    """[M, K] activation codes of graph input ``index`` (gen_quant_chain.py:253-274;
+    gen_u8i8_chain.py:68-73 for u8i8):
+
+    * ``default``: element i (row-major) = (37 i + seed) mod 2^act_bits, seed = (index + 1) * 374761393;
+    * ``zp``: every element the zero point 2^(act_bits - 1);
+    * ``k_impulse``: the zero point, except column ``impulse_k mod K`` = zero point + 1.
+    """
+    dt = np.dtype("<u2") if act_bits == 16 else np.dtype("uint8")
+    mask = (1 << act_bits) - 1
+    zp = 1 << (act_bits - 1)
+    if mode == "zp":
+        return np.full((m, k), zp, dtype=dt)
+    if mode == "k_impulse":
+        a = np.full((m, k), zp, dtype=dt)
+        a[:, impulse_k % k] = zp + 1
+        return a
+    if mode != "default":
+        raise ValueError(f"unknown activation mode {mode!r}")
+    seed = (index + 1) * GRAPH_SEED_STRIDE
+    i = np.arange(m * k, dtype=np.int64)
+    return ((i * 37 + seed) & mask).astype(dt).reshape(m, k)
+
+
+def graph_weight_kn(weight_bits: int, k: int, n: int, limit: Optional[int] = None) -> np.ndarray:
+    """[K, N] integer weight codes ((31 k + 13 n) mod (2 q + 1)) - q, q = 2^(weight_bits - 1) - 1
+    (or min(q, limit)) (gen_quant_chain.py:277-282; u8i8 uses the q = 7 pattern,
+    gen_u8i8_chain.py:173-174)."""
+    q = (1 << (weight_bits - 1)) - 1
+    if limit is not None:
+        q = max(1, min(q, int(limit)))
+    kk = np.arange(k, dtype=np.int64)[:, None]
+    nn = np.arange(n, dtype=np.int64)[None, :]
+    return (((kk * 31 + nn * 13) % (2 * q + 1)) - q).astype(np.int32)
+
+
+def graph_lpbq_block_scales(kernel_family: str, k: int, n: int, block: int) -> np.ndarray:
+    """[N, K / block] LPBQ integer block scales in {1, 2, 3} (gen_quant_chain.py:316-329):
+    w4a8: 1 + ((3 p + 5 b) mod 3) with p = 32 (n // 64) + n mod 32; w4a16: 1 + ((3 n + 5 (b // 2)) mod 3)."""
+    if k % block:
+        raise ValueError(f"LPBQ K={k} must be divisible by block size {block}")
+    nn = np.arange(n, dtype=np.int64)[:, None]
+    bb = np.arange(k // block, dtype=np.int64)[None, :]
+    if kernel_family == "w4a8":
+        pair = (nn // 64) * 32 + nn % 32
+        f = 1 + (pair * 3 + bb * 5) % 3
+    else:
+        f = 1 + (nn * 3 + (bb // 2) * 5) % 3
+    return f.astype(np.uint8)
+
+
+@dataclass
+class GraphCase:
+    """Operands and expected-output contract of one of the reference's CHAIN graphs."""
+
+    name: str
+    act_bits: int
+    weight_bits: int
+    out_bits: int
+    activation: np.ndarray         # [M, K] codes
+    weight_kn: np.ndarray          # [K, N] integer codes (LPBQ: before the block scales)
+    weight_compute_kn: np.ndarray  # [K, N] the integer weight the contract multiplies
+    bias_q: np.ndarray             # [N] int32 (the legacy contract adds it; native ignores it)
+    contract: str                  # "legacy" or "native"
+    chain: int                     # the reference's CI chain length for this family
+    lpbq_block_scale: Optional[np.ndarray] = None  # [N, K / block] uint8
+    lpbq_block: int = 0
+    kernel_family: str = ""
+
+    @property
+    def act_zp(self) -> int:
+        return 1 << (self.act_bits - 1)
+
+    @property
+    def out_zp(self) -> int:
+        return 32768 if self.out_bits == 16 else 0
+
+
+# name: (act bits, weight bits, out bits, kernel family, LPBQ, contract, CI chain) -- the families of
+# run_qnn_kernel_e2e_ci.sh:108-330 with their run-script defaults: the A8 flows use the legacy
+# contract with bias 1..N (bias layout "legacy", gen_quant_chain.py:869-873), the A16 flows the
+# native contract (run_w8a16_chain.sh / run_w4a16_chain.sh: --reference-contract native, a native
+# A16 bias layout whose bias_q is zero); W4A16 per-channel gates CHAIN=1 (its precision suite),
+# the others CHAIN=8; LPBQ blocks are 32 deep (--w4-lpbq-block-size default).
+GRAPH_FAMILIES = {
+    "u8i8": (8, 8, 8, "u8i8", False, "legacy", 8),
+    "w4a8_per_channel": (8, 4, 8, "w4a8", False, "legacy", 8),
+    "w4a8_lpbq": (8, 4, 8, "w4a8", True, "legacy", 8),
+    "w8a16": (16, 8, 16, "w8a16", False, "native", 8),
+    "w4a16_per_channel": (16, 4, 16, "w4a16", False, "native", 1),
+    "w4a16_lpbq": (16, 4, 16, "w4a16", True, "native", 8),
+    "w16a16": (16, 16, 16, "w16a16", False, "native", 8),
+}
+
+# The W4A16 precision suite of run_qnn_kernel_e2e_ci.sh:429-455: (activation mode, impulse column).
+W4A16_PRECISION_SUITE = {
+    "default": ("default", 0),
+    "zp": ("zp", 0),
+    "k_impulse0": ("k_impulse", 0),
+    "k_impulse1": ("k_impulse", 1),
+    "k_impulse7": ("k_impulse", 7),
+}
+
+
+def graph_case(name: str, m: int = 256, k: int = 256, n: int = 256, mode: str = "default", impulse_k: int = 0,
+               lpbq_block: int = 32) -> GraphCase:
+    """The operands of the reference's ``name`` CHAIN graph at M x K x N (gen_quant_chain.py:1078-1098,
+    gen_u8i8_chain.py:170-213)."""
+    a_bits, w_bits, o_bits, kfam, lpbq, contract, chain = GRAPH_FAMILIES[name]
+    # u8i8 carries int8 storage but its graph weights are the q = 7 pattern
+    w = graph_weight_kn(4 if name == "u8i8" else w_bits, k, n)
+    scales = None
+    wc = w
+    if lpbq:
+        scales = graph_lpbq_block_scales(kfam, k, n, lpbq_block)
+        wc = w * np.repeat(scales.T.astype(np.int32), lpbq_block, axis=0)
+    bias = np.arange(1, n + 1, dtype=np.int32) if contract == "legacy" else np.zeros(n, np.int32)
+    return GraphCase(name=name, act_bits=a_bits, weight_bits=w_bits, out_bits=o_bits,
+                     activation=graph_activation(a_bits, m, k, 0, mode, impulse_k), weight_kn=w,
+                     weight_compute_kn=wc.astype(np.int32), bias_q=bias, contract=contract, chain=chain,
+                     lpbq_block_scale=scales, lpbq_block=lpbq_block if lpbq else 0, kernel_family=kfam)

@@ -128,8 +128,14 @@ qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t cha
     if (scratch_dev == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: chain > 1 needs scratch");
     if (reinterpret_cast<uintptr_t>(out_dev) % 16 || reinterpret_cast<uintptr_t>(scratch_dev) % 16)
       return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: out and scratch must be 16-byte aligned");
-    if (scratch_dev == out_dev || scratch_dev == act_dev || out_dev == act_dev)
-      return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: act, out and scratch must be distinct");
+    // the three byte ranges must not overlap: act [M x K], out and scratch [M x N] each
+    const uintptr_t a = reinterpret_cast<uintptr_t>(act_dev), o = reinterpret_cast<uintptr_t>(out_dev),
+                    s = reinterpret_cast<uintptr_t>(scratch_dev);
+    const uintptr_t na = static_cast<uintptr_t>(m) * sh.K * (sh.act_bits == 16 ? 2 : 1);
+    const uintptr_t no = static_cast<uintptr_t>(m) * sh.N * (sh.out_bits == 16 ? 2 : 1);
+    auto overlap = [](uintptr_t p, uintptr_t np, uintptr_t q, uintptr_t nq) { return p < q + nq && q < p + np; };
+    if (overlap(a, na, o, no) || overlap(a, na, s, no) || overlap(o, no, s, no))
+      return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: act, out and scratch ranges must not overlap");
   }
   const void *src = act_dev;
   for (uint32_t i = 0; i < chain; ++i) {

@@ -95,8 +95,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <bool ASM>
 __device__ __forceinline__ void load_lds16(const uint8_t *base, uint32_t off, void *lds_wave_base) {
   if (ASM) {
+    // the LDS address goes in as an m0 operand, so the compiler sets m0 itself and knows it
+    // is live (the builtin loads rely on compiler-managed m0 too)
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_wave_base)));
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0v), "v"(off), "s"(base) : "memory");
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0v) : "memory");
   } else {
     __builtin_amdgcn_global_load_lds((gbl_void_ptr)(const_cast<uint8_t *>(base + off)), (lds_void_ptr)(lds_wave_base), 16, 0, 0);
   }

@@ -26,6 +26,7 @@
 // time, from the weight words the lanes still hold (handed over through LDS) and the constants
 // already staged: the fixup makes no global memory request.
 
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -559,16 +560,19 @@ int cu_count() { return device_cu_count(); }
 template <bool A16, bool LPBQ, int MM, int S>
 qh_status launch_unit(const UnitArgs &g, size_t dyn, hipStream_t stream) {
   const auto kernel = &qmm_gemv_unit_kernel<A16, LPBQ, MM, S>;
-  static bool attr_set[64] = {false};
+  // bit d: the dynamic-LDS limit is raised on device d (set once per device and instantiation;
+  // threads that race here both set the same attribute, which is harmless)
+  static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev < 0 || dev >= 64) return fail(QH_STATUS_UNSUPPORTED, "GEMV: device index %d", dev);
-  if (!attr_set[dev]) {
+  const uint64_t bit = uint64_t{1} << dev;
+  if (!(attr_set.load(std::memory_order_acquire) & bit)) {
     e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                             150 * 1024);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(qmm_gemv_unit_kernel)");
-    attr_set[dev] = true;
+    attr_set.fetch_or(bit, std::memory_order_release);
   }
   hipLaunchKernelGGL(kernel, dim3(g.G), dim3(kUT), dyn, stream, g);
   e = hipGetLastError();
@@ -586,15 +590,16 @@ qh_status launch_s(const UnitArgs &g, int S, size_t dyn, hipStream_t stream) {
 }  // namespace
 
 int device_cu_count() {
-  static int cached[64] = {0};
+  // per device; 0 = not queried yet (concurrent first queries store the same value)
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 qh_status launch_qmm_gemv_unit(const qh_qmm_prepared *p, int m, const void *act, void *out, hipStream_t stream) {

@@ -15,6 +15,7 @@ Mirrors the reference's solve entry points:
 
 from __future__ import annotations
 
+import contextlib
 from typing import Optional
 
 import torch
@@ -36,6 +37,19 @@ def _stream(stream):
     return int(s.cuda_stream)
 
 
+def _on(stream):
+    """Context in which tensors are allocated (and torch work is queued) on the launch stream, so
+    the caching allocator never hands a temporary to other streams' work while kernels on
+    ``stream`` still read it."""
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+
+
+def _same_device(device: torch.device, **tensors) -> None:
+    for name, x in tensors.items():
+        if x is not None and x.device != device:
+            raise TypeError(f"{name} must be on {device}, got {x.device}")
+
+
 def gdn_solve(A: torch.Tensor, precision: int = FP32, out: Optional[torch.Tensor] = None,
               stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
     """T = (I - A)^-1 for float32 A [..., C, C] (strictly lower triangle used)."""
@@ -46,7 +60,8 @@ def gdn_solve(A: torch.Tensor, precision: int = FP32, out: Optional[torch.Tensor
         raise ValueError("A must be square in its last two dims")
     heads = A.numel() // (C * C)
     if out is None:
-        out = torch.empty_like(A)
+        with _on(stream):
+            out = torch.empty_like(A)
     st = _lib.lib().qh_gdn_solve_f32(A.data_ptr(), out.data_ptr(), heads, C, precision, _stream(stream))
     _lib.check(st, "qh_gdn_solve_f32")
     return out
@@ -83,9 +98,11 @@ def gdn_chunk_uw(k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.
         raise ValueError("k, v: [B, T, H, D]; g, beta: [B, T, H]")
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError("out_dtype must be bfloat16 or float32")
+    _same_device(k.device, v=v, g=g, beta=beta)
     B, T, H, D = k.shape
-    w = torch.empty((B, T, H, D), dtype=out_dtype, device=k.device)
-    u = torch.empty_like(w)
+    with _on(stream):
+        w = torch.empty((B, T, H, D), dtype=out_dtype, device=k.device)
+        u = torch.empty_like(w)
     flags = (W_DECAY if decay_w else 0) | (_lib.QH_GDN_OUT_F32 if out_dtype == torch.float32 else 0)
     st = _lib.lib().qh_gdn_chunk_uw_ex(k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), w.data_ptr(),
                                        u.data_ptr(), B, T, H, D, chunk, flags, int(max_workgroups), _stream(stream))
@@ -118,11 +135,14 @@ def gdn_chunk_state(q: torch.Tensor, k: torch.Tensor, g: torch.Tensor, w: torch.
         raise ValueError("q, k, w, u: [B, T, H, D]; g: [B, T, H]")
     B, T, H, D = q.shape
     if initial_state is not None:
-        if (initial_state.dtype != torch.float32 or not initial_state.is_contiguous()
-                or tuple(initial_state.shape) != (B, H, D, D)):
+        if (not isinstance(initial_state, torch.Tensor) or initial_state.dtype != torch.float32
+                or not initial_state.is_contiguous() or tuple(initial_state.shape) != (B, H, D, D)):
             raise TypeError("initial_state must be a contiguous float32 [B, H, D, D] tensor")
-    o = torch.empty((B, T, H, D), dtype=out_dtype, device=q.device)
-    s_out = torch.empty((B, H, D, D), dtype=torch.float32, device=q.device)
+    # every operand on q's device: a host tensor's address would be dereferenced by the kernel
+    _same_device(q.device, k=k, g=g, w=w, u=u, initial_state=initial_state)
+    with _on(stream):
+        o = torch.empty((B, T, H, D), dtype=out_dtype, device=q.device)
+        s_out = torch.empty((B, H, D, D), dtype=torch.float32, device=q.device)
     flags = (_lib.QH_GDN_WU_F32 if w.dtype == torch.float32 else 0) | (
         _lib.QH_GDN_OUT_F32 if out_dtype == torch.float32 else 0)
     st = _lib.lib().qh_gdn_chunk_state(q.data_ptr(), k.data_ptr(), g.data_ptr(), w.data_ptr(), u.data_ptr(),
@@ -141,12 +161,16 @@ def gdn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tens
     to whole chunks of 64, which leaves o and S unchanged.  Stage A runs with float32 W, U for
     ``FP32`` and bf16 for ``BF16``."""
     B, T, H, D = q.shape
-    pad = (-T) % STATE_CHUNK
-    if pad:
-        F = torch.nn.functional
-        q, k, v = (F.pad(x, (0, 0, 0, 0, 0, pad)).contiguous() for x in (q, k, v))
-        g, beta = (F.pad(x, (0, 0, 0, pad)).contiguous() for x in (g, beta))
-    wu_dtype = torch.float32 if precision == FP32 else torch.bfloat16
-    w, u = gdn_chunk_uw(k, v, g, beta, STATE_CHUNK, decay_w=True, out_dtype=wu_dtype, stream=stream)
-    o, s = gdn_chunk_state(q, k, g, w, u, initial_state, precision, out_dtype, stream)
-    return (o[:, :T].contiguous() if pad else o), s
+    _same_device(q.device, k=k, v=v, g=g, beta=beta, initial_state=initial_state)
+    # the padded inputs and the stage-A outputs are temporaries: allocated (and padded) on the
+    # launch stream, so they stay reserved until the kernels queued there have read them
+    with _on(stream):
+        pad = (-T) % STATE_CHUNK
+        if pad:
+            F = torch.nn.functional
+            q, k, v = (F.pad(x, (0, 0, 0, 0, 0, pad)).contiguous() for x in (q, k, v))
+            g, beta = (F.pad(x, (0, 0, 0, pad)).contiguous() for x in (g, beta))
+        wu_dtype = torch.float32 if precision == FP32 else torch.bfloat16
+        w, u = gdn_chunk_uw(k, v, g, beta, STATE_CHUNK, decay_w=True, out_dtype=wu_dtype, stream=stream)
+        o, s = gdn_chunk_state(q, k, g, w, u, initial_state, precision, out_dtype, stream)
+        return (o[:, :T].contiguous() if pad else o), s

@@ -11,6 +11,7 @@ u8i8, w4a8_per_channel, w4a8_lpbq, w8a16, w4a16_per_channel, w4a16_lpbq.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes as C
 from typing import Optional
 
@@ -18,11 +19,11 @@ import numpy as np
 import torch
 
 from . import _lib
-from .cases import FAMILIES, Family, QmmCase
+from .cases import FAMILIES, Family, GraphCase, QmmCase
 
 PATH_AUTO, PATH_GEMM, PATH_GEMV = 0, 1, 2
 
-__all__ = ["QuantMatmul", "PATH_AUTO", "PATH_GEMM", "PATH_GEMV", "CONTRACTS", "weight_format_of"]
+__all__ = ["QuantMatmul", "PATH_AUTO", "PATH_GEMM", "PATH_GEMV", "CONTRACTS", "weight_format_of", "graph_contract"]
 
 
 def weight_format_of(family: Family) -> int:
@@ -46,9 +47,31 @@ CONTRACTS = {
 }
 
 
+def graph_contract(gc: GraphCase) -> tuple:
+    """(contract name, divisor) of qh_qmm_run_contract that is a graph's reference step
+    (gen_quant_chain.py:971-996): legacy -> int32 clip with the bias; native W4A16 -> the
+    accumulator floored to a multiple of 256, then rint(acc / 7 + 32768); other native A16 ->
+    rint(acc / qmax + 32768) with qmax = 2^(weight bits - 1) - 1 (127 for W8A16, 32767 for W16A16)."""
+    if gc.contract == "legacy":
+        return "clip_i32", 1
+    qmax = (1 << (gc.weight_bits - 1)) - 1
+    if gc.kernel_family == "w4a16":
+        return "floor256_div_rint", qmax
+    return "div_rint", qmax
+
+
 def _stream_ptr(stream: Optional[torch.cuda.Stream]) -> int:
     s = stream if stream is not None else torch.cuda.current_stream()
     return int(s.cuda_stream)
+
+
+def _overlaps(a: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> bool:
+    """True if the byte ranges of two contiguous tensors overlap."""
+    if a is None or b is None:
+        return False
+    pa, pb = a.data_ptr(), b.data_ptr()
+    na, nb = a.numel() * a.element_size(), b.numel() * b.element_size()
+    return pa < pb + nb and pb < pa + na
 
 
 class QuantMatmul:
@@ -154,6 +177,33 @@ class QuantMatmul:
             device=device,
         )
 
+    @classmethod
+    def from_graph_case(cls, gc: GraphCase, device=None) -> "QuantMatmul":
+        """The prepared op of one of the reference's CHAIN graphs (integer operands; the scales are
+        unused by the integer contracts its outputs follow, so they are 1)."""
+        n = gc.weight_kn.shape[1]
+        if gc.weight_bits == 16:
+            fmt = _lib.QH_WEIGHT_I16
+        elif gc.lpbq_block_scale is not None:
+            fmt = _lib.QH_WEIGHT_I4_LPBQ
+        else:
+            fmt = _lib.QH_WEIGHT_I8 if gc.weight_bits == 8 or gc.name == "u8i8" else _lib.QH_WEIGHT_I4
+        return cls(
+            np.ascontiguousarray(gc.weight_kn.T),
+            np.ones(n, np.float32),
+            gc.bias_q,
+            act_bits=gc.act_bits,
+            out_bits=gc.out_bits,
+            act_scale=1.0,
+            out_scale=1.0,
+            act_zp=gc.act_zp,
+            out_zp=gc.out_zp,
+            weight_format=fmt,
+            lpbq_block_scale=gc.lpbq_block_scale,
+            lpbq_block=gc.lpbq_block,
+            device=device,
+        )
+
     # ------------------------------------------------------------------ execution
     def _check_act(self, act: torch.Tensor) -> int:
         if not isinstance(act, torch.Tensor) or act.device.type != "cuda":
@@ -164,13 +214,24 @@ class QuantMatmul:
             raise ValueError(f"activation must be contiguous [M, {self.k}], got {tuple(act.shape)}")
         return act.shape[0]
 
+    def _check_out(self, out: torch.Tensor, m: int, device: torch.device, what: str) -> None:
+        """A caller-supplied output (or chain scratch) buffer: [m, N] of the output dtype,
+        contiguous, on the activation's device."""
+        if not isinstance(out, torch.Tensor) or out.device != device:
+            raise TypeError(f"{what} must be a tensor on {device}")
+        if tuple(out.shape) != (m, self.n) or out.dtype != self.out_dtype or not out.is_contiguous():
+            raise ValueError(f"{what} must be contiguous [{m}, {self.n}] {self.out_dtype}, got "
+                             f"{tuple(out.shape)} {out.dtype}")
+
     def __call__(self, act: torch.Tensor, out: Optional[torch.Tensor] = None, path: int = PATH_AUTO,
                  stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
         m = self._check_act(act)
         if out is None:
             out = torch.empty((m, self.n), dtype=self.out_dtype, device=act.device)
-        elif out.shape != (m, self.n) or out.dtype != self.out_dtype or not out.is_contiguous():
-            raise ValueError("bad output tensor")
+        else:
+            self._check_out(out, m, act.device, "output")
+            if _overlaps(act, out):
+                raise ValueError("the activation must not overlap the output")
         st = _lib.lib().qh_qmm_run_path(self._h, m, act.data_ptr(), out.data_ptr(), path, _stream_ptr(stream))
         _lib.check(st, "qh_qmm_run")
         return out
@@ -191,8 +252,10 @@ class QuantMatmul:
         cid = CONTRACTS[contract] if isinstance(contract, str) else int(contract)
         if out is None:
             out = torch.empty((m, self.n), dtype=self.out_dtype, device=act.device)
-        elif out.shape != (m, self.n) or out.dtype != self.out_dtype or not out.is_contiguous():
-            raise ValueError("bad output tensor")
+        else:
+            self._check_out(out, m, act.device, "output")
+            if _overlaps(act, out):
+                raise ValueError("the activation must not overlap the output")
         st = _lib.lib().qh_qmm_run_contract(self._h, m, act.data_ptr(), out.data_ptr(), cid, int(divisor),
                                             _stream_ptr(stream))
         _lib.check(st, "qh_qmm_run_contract")
@@ -206,10 +269,23 @@ class QuantMatmul:
         m = self._check_act(act)
         cid = _lib.QH_CONTRACT_NONE if contract is None else (CONTRACTS[contract] if isinstance(contract, str)
                                                                else int(contract))
+        if int(chain) < 1:
+            raise ValueError(f"chain must be >= 1, got {chain}")
         if out is None:
             out = torch.empty((m, self.n), dtype=self.out_dtype, device=act.device)
+        else:
+            self._check_out(out, m, act.device, "output")
         if scratch is None and chain > 1:
-            scratch = torch.empty_like(out)
+            # allocated on the launch stream, so the caching allocator cannot hand it to other
+            # work on the current stream while the chain still uses it
+            with torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext():
+                scratch = torch.empty_like(out)
+        elif scratch is not None:
+            self._check_out(scratch, m, act.device, "scratch")
+        if chain > 1 and _overlaps(out, scratch):
+            raise ValueError("out and scratch must not overlap")
+        if _overlaps(act, out) or (chain > 1 and _overlaps(act, scratch)):
+            raise ValueError("the activation must not overlap out or scratch")
         st = _lib.lib().qh_qmm_run_chain(self._h, m, int(chain), act.data_ptr(), out.data_ptr(),
                                          scratch.data_ptr() if scratch is not None else None, cid, int(divisor),
                                          _stream_ptr(stream))

@@ -141,6 +141,28 @@ def test_torch_stage_a_matches_lapack_products(decay_w):
     assert og.oc(W.numpy(), Wref) < 1e-12
 
 
+@pytest.mark.parametrize("C", [16, 64, 256])
+@pytest.mark.parametrize("decay_w", [False, True])
+def test_stage_a_triangular_solve_form_matches_recurrence(decay_w, C):
+    """chunk_stage_a_solve_torch (batched unit-lower solve, used for the full-size checks) equals the
+    row recurrence of the reference kernel and the LAPACK inverse, and a wrong decay sign is caught."""
+    import torch
+
+    rng = np.random.default_rng(C + decay_w)
+    n = 3
+    k = rng.standard_normal((n, C, 128))
+    v = rng.standard_normal((n, C, 128))
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((n, C))))
+    gc = -np.logaddexp(0.0, -(rng.standard_normal((n, C)) + 3.0))
+    U, W = og.chunk_stage_a_solve_torch(k, v, gc, beta, decay_w=decay_w)
+    U2, W2 = og.chunk_stage_a_torch(k, v, gc, beta, decay_w=decay_w)
+    Uref, Wref = og.chunk_uw(og.inverse_fp64(og.build_A(k, beta, gc)), k, v, beta, gc, decay_w=decay_w)
+    for X, R in ((U, U2), (W, W2), (U, Uref), (W, Wref)):
+        assert og.oc(np.asarray(X), np.asarray(R)) < 1e-11
+    Ubad, _ = og.chunk_stage_a_solve_torch(k, v, -gc, beta, decay_w=decay_w)
+    assert og.oc(Ubad.numpy(), Uref) > 1e-3
+
+
 def _seq_inputs(n=3, T=100, D=16, seed=0):
     rng = np.random.default_rng(seed)
     q, k, v = (rng.standard_normal((n, T, D)) for _ in range(3))
@@ -183,18 +205,27 @@ def test_chunk_state_plausible_mistakes_are_caught(plant):
 
 
 @pytest.mark.skipif(not (REF_DIR / "gdn_test_core").exists(), reason="oracle/_ref not built (needs /root/reference)")
+@pytest.mark.parametrize("case", ["config4", "full_range"])
 @pytest.mark.parametrize("C", [16, 32, 64])
-def test_int16_op_model_matches_reference_core(tmp_path, C):
+def test_int16_op_model_matches_reference_core(tmp_path, C, case):
     """solve_int16_op reproduces the op core's int8 output codes (gdn_solve_core.h through its
-    own host driver test_core.cpp, sTout = 1/127) code for code."""
+    own host driver test_core.cpp, sTout = 1/127) code for code.  ``full_range``: strictly-lower
+    codes uniform over [-32767, 32767] at a small scale, which drive the int16 clip and the
+    int32 wrap-around of the diagonal solves (the GPU op-model test's full-range case)."""
     H = 3
-    k, beta, gc = og.config4_inputs(heads=H, C=C, seed=17 + C)
-    A = og.build_A(k, beta, gc)
     codes, sAs = [], []
-    for h in range(H):
-        q, s = _int16_codes(A[h])
-        codes.append(q)
-        sAs.append(s)
+    if case == "config4":
+        k, beta, gc = og.config4_inputs(heads=H, C=C, seed=17 + C)
+        A = og.build_A(k, beta, gc)
+        for h in range(H):
+            q, s = _int16_codes(A[h])
+            codes.append(q)
+            sAs.append(s)
+    else:
+        rng = np.random.default_rng(C)
+        for h in range(H):
+            codes.append(np.tril(rng.integers(-32767, 32768, (C, C)), -1).astype(np.int16))
+            sAs.append(3e-5)
     np.array([H, C], np.int32).tofile(tmp_path / "dims.i32")
     np.stack(codes).astype(np.int16).tofile(tmp_path / "A_codes.i16")
     np.array(sAs, np.float32).tofile(tmp_path / "sA.f32")

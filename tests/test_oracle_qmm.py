@@ -315,3 +315,18 @@ def test_u8_drain_contract_closed_forms():
     shifted = qmm.contract_output(acc, "u8_drain", _drain_param(1.0, 0x1280), bias).astype(np.int64)
     np.testing.assert_array_equal(shifted, np.clip(np.clip(np.trunc(d / 512.0), -(1 << 40), 1 << 40) + (0x1280 >> 7), 0, 255))
     assert base.max() <= 255
+
+
+def test_uniform_fixed_scale_case_parameters():
+    """uniform_u8i8_case carries the stated constants and distributions, and its outputs reach both
+    clip rails and the interior (so a GPU comparison exercises clipping and rounding)."""
+    c = C.uniform_u8i8_case(256, 256, 256, seed=1)
+    assert c.family.name == "u8i8" and c.act_zp == 128 and c.out_zp == 0
+    assert c.act_scale == 0.02 and c.out_scale == 0.05
+    assert np.all(c.weight_scale == np.float32(0.01))
+    assert c.activation_q.dtype == np.uint8 and c.activation_q.min() == 0 and c.activation_q.max() == 255
+    assert c.weight_q_nk.min() == -127 and c.weight_q_nk.max() == 127
+    assert np.abs(c.bias_q).max() <= 1 << 15 and np.abs(c.bias_q).max() > 1 << 14
+    assert np.array_equal(c.weight_deq, c.weight_q_nk.astype(np.float32) * np.float32(0.01))
+    out = qmm.expected_output_case(c)
+    assert (out == 0).any() and (out == 255).any() and ((out > 0) & (out < 255)).any()

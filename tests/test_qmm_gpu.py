@@ -256,3 +256,16 @@ def test_gemv_near_tie_decode_rows_bit_exact(gpu, fam, k, rows):
         return
     got = run(c, gpu, path=2, rows=rows)
     assert np.array_equal(got, want), f"gemv: {diff_msg(got, want)}"
+
+
+@pytest.mark.parametrize("path,rows", [(1, 256), (0, 256), (2, 1), (2, 16), (1, 100)],
+                         ids=["gemm", "auto", "gemv_m1", "gemv_m16", "gemm_ragged"])
+def test_uniform_fixed_scale_u8i8_bit_exact(gpu, path, rows):
+    """The u8i8 matmul as stated with fixed per-tensor parameters (U[0,255] activations at 0.02 /
+    zero point 128, U[-127,127] weights at 0.01, bias U(+-2^15), output 0.05 / 0): 256^3, every
+    output (most on the clip rails) equal to the oracle's."""
+    c = C.uniform_u8i8_case(256, 256, 256, seed=1)
+    want = oq.expected_output_case(c)[:rows]
+    print(f"[qmm] uniform u8i8 path={path} rows={rows}", flush=True)
+    got = run(c, gpu, path=path, rows=rows)
+    assert np.array_equal(got, want), diff_msg(got, want)

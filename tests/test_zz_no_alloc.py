@@ -64,3 +64,42 @@ def test_chain_noalloc_rejects_outputs_beyond_the_static_scratch(gpu):
     assert st == _lib.QH_STATUS_SHAPE_UNSUPPORTED
     assert b"static scratch" in _lib.lib().qh_last_error()
     op.close()
+
+
+def test_chain_noalloc_under_graph_capture(gpu):
+    """The use the entry point exists for: captured into a HIP graph (no allocation is possible
+    during capture), replayed several times with eager work in between, every replay equal to
+    the chain with a caller scratch buffer run eagerly."""
+    import torch
+
+    from qcom_htp_amd import _lib
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    L = _lib.lib()
+    c = cases.make_case("w4a8_lpbq", "normal_random", 256, 256, 256)
+    op = QuantMatmul.from_case(c, device=gpu)
+    act = torch.from_numpy(c.activation_q).to(gpu)
+    m, chain = 256, 4
+    print(f"[noalloc graph] w4a8_lpbq m={m} chain={chain}", flush=True)
+    want = torch.empty((m, op.n), dtype=op.out_dtype, device=gpu)
+    scr = torch.empty_like(want)
+    _lib.check(L.qh_qmm_run_chain(op._h, m, chain, act.data_ptr(), want.data_ptr(), scr.data_ptr(), 0xFFFFFFFF, 1,
+                                  torch.cuda.current_stream().cuda_stream), "qh_qmm_run_chain")
+    out = torch.zeros_like(want)
+    other_act = act.flip(0).contiguous()
+    other_out = torch.empty_like(want)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.check(L.qh_qmm_run_chain_noalloc(op._h, m, chain, act.data_ptr(), out.data_ptr(), 0xFFFFFFFF, 1,
+                                              torch.cuda.current_stream().cuda_stream), "noalloc (capture)")
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep}: {int((out != want).sum())} mismatches"
+        # eager work between replays, which also overwrites the shared static array
+        _lib.check(L.qh_qmm_run_chain_noalloc(op._h, m, chain, other_act.data_ptr(), other_out.data_ptr(), 0xFFFFFFFF,
+                                              1, torch.cuda.current_stream().cuda_stream), "noalloc (eager)")
+        torch.cuda.synchronize()
+    op.close()
