@@ -47,11 +47,18 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
+# Sources whose device assembly is kept and checked (qcom_htp_amd.isa_check): the GEMM's k loop
+# counts its own memory waits.
+ISA_CHECKED = ("qmm_gemm.hip",)
+
+
 def _compile(src: Path) -> Path:
     obj = OBJDIR / (src.name + ".o")
     cmd = [_hipcc(), *COMMON]
     if src.suffix == ".hip":
         cmd += ["-x", "hip", *HIP_FLAGS]
+        if src.name in ISA_CHECKED:
+            cmd += ["-save-temps=obj"]
     else:
         cmd += ["-D__HIP_PLATFORM_AMD__"]
     cmd += ["-c", str(src), "-o", str(obj)]
@@ -62,7 +69,20 @@ def _compile(src: Path) -> Path:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{err}")
     if err.strip():
         print(err, file=sys.stderr)
+    if src.name in ISA_CHECKED:
+        from .isa_check import check_file
+
+        asm = device_asm(src)
+        names, errs = check_file(str(asm))
+        if not names or errs:
+            raise RuntimeError(f"{src.name}: memory-wait check of {asm.name} failed "
+                               f"({len(names)} kernels):\n" + "\n".join(errs[:20]))
     return obj
+
+
+def device_asm(src: Path) -> Path:
+    """The gfx950 assembly that -save-temps=obj left for ``src`` in the build folder."""
+    return OBJDIR / f"{src.stem}-hip-amdgcn-amd-amdhsa-{ARCH}.s"
 
 
 def build(verbose: bool = True) -> Path:

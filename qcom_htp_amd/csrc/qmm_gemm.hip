@@ -7,13 +7,16 @@
 // conversions run under the other's MFMAs (a lone wave stalls its MFMAs on its own LDS reads).
 // K is consumed 128 deep per pipeline step.
 //
-// Data movement: every operand tile goes global -> LDS with direct-to-LDS loads
-// (global_load_lds_dwordx4), bypassing VGPRs; both stages are in flight and one barrier per
-// 128-k tile both publishes the landed tile and frees the stage read before.  Weight tiles are
-// int8 (int4 codes and LPBQ code * block scale are widened at prepare time) and prepared as
-// the exact LDS image (pre-swizzled); activation tiles are gathered into the swizzled layout
-// by the per-lane source addresses.  Activations are converted on the MFMA fragments after
-// the LDS read:
+// Data movement: activation tiles go global -> LDS with direct-to-LDS loads
+// (global_load_lds_dwordx4), bypassing VGPRs, gathered into a swizzled layout by the per-lane
+// source addresses; both stages are in flight and one barrier per 128-k tile both publishes the
+// landed tile and frees the stage read before.  Weight tiles are int8 (int4 codes and LPBQ
+// code * block scale are widened at prepare time) prepared in MFMA fragment order, so each
+// wave loads its weight fragments straight into registers (one coalesced 1 KiB load per
+// fragment, three 32-k steps ahead) and LDS carries only the activations: per 32-k step a CU
+// reads 32 KiB of fragments from LDS and its DMA writes 8 KiB (with the weights through LDS too
+// it was 48 + 16 KiB, about the LDS bandwidth during the step's MFMAs).  Activations are
+// converted on the MFMA fragments after the LDS read:
 //   * 8-bit activations: XOR 0x80 gives the signed a - 128;
 //   * 16-bit activations a - 32768 = 256*hi + lo' + 128: the hi and lo' bytes of each u16
 //     become two int8 fragments, each multiplied into its own accumulator.
@@ -68,10 +71,14 @@ constexpr int kNT = 2;         // 32-column MFMA blocks per wave
 
 struct Cfg {
   static constexpr int kTileB = 32768;  // 256 operand columns x 128 k, int8
-  static constexpr int kStages = 2;
-  static constexpr int kLoadsA = kTileA / (16 * kGemmThreads);  // 16-byte loads per thread per stage
-  static constexpr int kLoadsB = kTileB / (16 * kGemmThreads);
-  static constexpr int kLoads = kLoadsA + kLoadsB;  // per wave per stage
+#ifndef QH_GEMM_STAGES
+#define QH_GEMM_STAGES 2
+#endif
+  static constexpr int kStages = QH_GEMM_STAGES;  // activation tiles in LDS (the DMA runs S - 1 tiles ahead)
+  static constexpr int kLoadsA = kTileA / (16 * kGemmThreads);  // 16-byte DMA loads per thread per stage
+  // Weight fragments: kNT 16-byte loads per lane per 32-k step, into a ring of kBRing step slots,
+  // requested kBRing - 1 steps ahead of their MFMAs.
+  static constexpr int kBRing = 4;
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -192,6 +199,7 @@ __device__ __forceinline__ uint4 load_w16_raw(const GemmArgs &g, int cb, int k) 
 }
 __device__ __forceinline__ int w_at(const uint4 &v, int j) { return reinterpret_cast<const int8_t *>(&v)[j]; }
 
+
 // Exact float64 recomputation of one output, term by term as the oracle forms it:
 // sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), then + bias_deq, / sO, + out_zp, rint, clip.
 template <bool A16>
@@ -265,13 +273,14 @@ __device__ __forceinline__ void tile_of(int w, int TM, int TN, int *tm, int *tn)
 // Everything the k loop needs about the workgroup's tile.
 struct MainCtx {
   const uint8_t *act;     // activations [M][K] (u8) or [M][K] (u16)
-  const uint8_t *btiles;  // weight tiles of this column panel, one per 128-k step
-  int M, K, m0, t, lane, wave, wm, wn;
+  const uint8_t *bw;      // weight tiles of this column panel (one per 128-k step), at the wave's quarter
+  uint32_t boff;          // this lane's byte offset inside a weight fragment (16 lane)
+  int M, K, KT, m0, t, lane, wave, wm, wn;
 };
 
-// Issue the direct-to-LDS loads of k-tile kt into the stage (wa, wb).
+// Issue the direct-to-LDS activation loads of k-tile kt into the stage wa.
 template <bool A16, bool ASM>
-__device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__restrict__ wa, uint8_t *__restrict__ wb) {
+__device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__restrict__ wa) {
   using C = Cfg;
   // 32-bit byte offsets from uniform bases: the tile's first activation row, the k-tile of
   // the weight panel (256 rows x K x 2 bytes < 2^32 for K < 2^23)
@@ -295,21 +304,37 @@ __device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__
     }
     load_lds16<ASM>(abase, off, wa + (j * kGemmThreads + c.wave * 64) * 16);
   }
-  const uint8_t *bsrc = c.btiles + static_cast<size_t>(kt) * C::kTileB;
-#pragma unroll
-  for (int j = 0; j < C::kLoadsB; ++j)
-    load_lds16<ASM>(bsrc, static_cast<uint32_t>(j * kGemmThreads + c.t) * 16u, wb + (j * kGemmThreads + c.wave * 64) * 16);
 }
 
-// Raw LDS words of one 32-k step: A fragments and B fragments.
+// The wave's weight fragments of 32-k step kk of k-tile kt (kt clamped to the last tile: past
+// the end the loads re-read it, so every step issues the same loads and wait counts stay fixed):
+// fragment nt of the wave's column quarter wn is the 1 KiB at 1 KiB * (8 kk + 2 wn + nt).
+// Issued from assembly, like the activation DMA, so that the issue order of all of the loop's
+// vector-memory requests is the program order and the loop's explicit wait counts are exact (the
+// compiler's own counts would not see the DMA and would wait for requests issued later).  The
+// registers receive their data only after a covering wait_b().
+__device__ __forceinline__ void load_b(const MainCtx &c, int kt, int kk, v4i (&b)[kNT]) {
+  const uint8_t *p = c.bw + static_cast<size_t>(min(kt, c.KT - 1)) * Cfg::kTileB + kk * 8192;
+  static_assert(kNT == 2, "two fragments per step");
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(b[0]) : "v"(c.boff), "s"(p));
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:1024" : "=v"(b[1]) : "v"(c.boff), "s"(p));
+}
+
+// s_waitcnt vmcnt(N) that the weight fragments b pass through: the MFMAs that read them depend
+// on this instruction, so they cannot move above it.
+template <int N>
+__device__ __forceinline__ void wait_b(v4i (&b)[kNT]) {
+  static_assert(kNT == 2 && N >= 0 && N < 64, "two fragments per step");
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(b[0]), "+v"(b[1]) : "n"(N));
+}
+
+// Raw LDS words of one 32-k step: the activation fragments.
 struct RawStep {
   uint4 a[4];
-  uint4 b[kNT];
 };
 
 template <bool A16>
-__device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__restrict__ la, const uint8_t *__restrict__ lb,
-                                          int kk, RawStep &r) {
+__device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__restrict__ la, int kk, RawStep &r) {
   const int s16 = 2 * kk + (c.lane >> 5);  // 16-k chunk index inside the 128-k tile
   if (!A16) {
     static_for<4>([&](auto mt) {
@@ -323,16 +348,11 @@ __device__ __forceinline__ void read_step(const MainCtx &c, const uint8_t *__res
       r.a[2 * mt + 1] = *reinterpret_cast<const uint4 *>(la + row * 256 + 16 * ((2 * s16 + 1) ^ swz16(row)));
     });
   }
-  static_for<kNT>([&](auto nt) {
-    const int col = c.wn * 64 + nt * 32 + (c.lane & 31);
-    r.b[nt] = *reinterpret_cast<const uint4 *>(lb + col * 128 + 16 * (s16 ^ swz8(col)));
-  });
 }
 
-// Raw words -> MFMA operands: activations to signed bytes (16-bit: hi / lo' byte planes); the
-// int8 weight words are used as they are.
+// Raw words -> MFMA operands: activations to signed bytes (16-bit: hi / lo' byte planes).
 template <bool A16>
-__device__ __forceinline__ void convert_step(const RawStep &r, v4i (&af)[4], v4i (&bf)[kNT]) {
+__device__ __forceinline__ void convert_step(const RawStep &r, v4i (&af)[4]) {
   if (!A16) {
     static_for<4>([&](auto mt) {
       const uint4 v = r.a[mt];
@@ -350,66 +370,70 @@ __device__ __forceinline__ void convert_step(const RawStep &r, v4i (&af)[4], v4i
                            static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
     });
   }
-  static_for<kNT>([&](auto nt) {
-    const uint4 v = r.b[nt];
-    bf[nt] = v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)};
-  });
 }
 
 // The k loop is a software pipeline over 32-k steps sigma = 4 kt + kk (kt: 128-k tile, kk: its
-// 32-k step): step sigma runs its MFMAs while the operands of step sigma + 1 are converted
-// (VALU) and the LDS fragments of step sigma + 2 are read, so the conversions issue in the
-// shadow of the matrix core rather than in bursts between MFMA groups.  Tiles: both stages
-// are filled up front; in step 2 of tile kt each wave has read all of tile kt, waits until
-// tile kt + 1 has landed, and one barrier then publishes tile kt + 1 and frees the stage of
-// tile kt, which receives tile kt + 2 at once.  The first two steps of tile kt + 1 are read
-// (and the first converted) during steps 2 and 3 of tile kt.
+// 32-k step): step sigma runs its MFMAs while the activations of step sigma + 1 are converted
+// (VALU), the LDS fragments of step sigma + 2 are read and the weight fragments of step
+// sigma + 3 are requested, so the conversions issue in the shadow of the matrix core rather
+// than in bursts between MFMA groups.  Tiles: both activation stages are filled up front; in
+// step 2 of tile kt each wave has read all of tile kt, waits until tile kt + 1 has landed, and
+// one barrier then publishes tile kt + 1 and frees the stage of tile kt, which receives tile
+// kt + 2 at once.  The first two steps of tile kt + 1 are read (and the first converted) during
+// steps 2 and 3 of tile kt.
 struct PipeRegs {
-  RawStep raw[2];    // LDS words of the steps sigma + 1 / sigma + 2 (slot sigma & 1)
-  v4i af[2][4];      // converted operands of steps sigma / sigma + 1 (slot sigma & 1)
-  v4i bf[2][kNT];
+  RawStep raw[2];        // LDS words of the steps sigma + 1 / sigma + 2 (slot sigma & 1)
+  v4i af[2][4];          // converted activations of steps sigma / sigma + 1 (slot sigma & 1)
+  v4i bq[Cfg::kBRing][kNT];  // weight fragments of steps sigma .. sigma + 3 (slot sigma % 4 = kk)
 };
 
-// Wait until at most n of this wave's tiles are still in flight.
-template <int LOADS>
-__device__ __forceinline__ void wait_tiles(int n) {
-  if (n >= 2)
-    wait_vmcnt<2 * LOADS>();
-  else if (n == 1)
-    wait_vmcnt<LOADS>();
-  else
-    wait_vmcnt<0>();
-}
 
 // Workgroup barrier that waits for this wave's LDS reads (not for its loads in flight, which
 // the release fence of __syncthreads would also wait for).
 __device__ __forceinline__ void lds_read_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// One 128-k tile kt in stage (la, lb); the next tile is in (na, nb).  On entry af/bf slot 0
-// hold the converted operands of step 0 and raw slot 1 the LDS words of step 1.
+// One 128-k tile kt in stage la; the next tile is in na.  On entry af slot 0 holds the converted
+// activations of step 0, raw slot 1 the LDS words of step 1, and bq slots 0..2 the weight
+// fragments of steps 0..2 (requested).
+//
+// Memory counter: the activation DMA and the weight loads share this wave's vector-memory
+// counter, which retires in issue order, and every request of the loop is issued from assembly
+// in program order, so each wait count below is the exact number of requests issued after the
+// one waited for.  Step kk issues, in order: [kk == 2: the DMA of tile kt + 2 (kLoadsA)] and the
+// weight loads of step sigma + 3 (kNT).  Step kk needs the weights of step sigma, loaded 3 steps
+// earlier, followed by the loads of two steps (2 kNT) and, for kk = 3 and 0 (the loads of kk = 0
+// and 1 of the tile before), the DMA issued at step 2 in between (kLoadsA more).  At kk = 2 the
+// same count also covers the DMA of tile kt + 1, issued before the weights waited for.
 template <bool A16>
-__device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t *__restrict__ la, uint8_t *__restrict__ lb,
-                                       const uint8_t *__restrict__ na, const uint8_t *__restrict__ nb, PipeRegs &p,
-                                       v16i (&acc)[4][kNT]) {
+__device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t *__restrict__ la,
+                                       const uint8_t *__restrict__ na, PipeRegs &p, v16i (&acc)[4][kNT]) {
   using C = Cfg;
   constexpr int S = C::kStages;
   static_for<4>([&](auto kkc) {
     constexpr int kk = decltype(kkc)::value;
+    // each step's loads stay in their step (the scheduler may not hoist or sink them across)
+    __builtin_amdgcn_sched_barrier(0);
+    // the weights of step sigma have landed (kk = 2: tile kt + 1's DMA too)
+    wait_b<(kk == 0 || kk == 3) ? 2 * kNT + C::kLoadsA : 2 * kNT>(p.bq[kk]);
     if (kk == 2) {
       // Every tile slot issues (past the end it reloads tile KT - 1 into a stage nobody reads
-      // again), so exactly S - 1 tiles are in flight here: let all but tile kt + 1 remain.
-      // The issue is not behind a branch, so its loads interleave with the MFMAs below.
-      wait_tiles<C::kLoads>(S - 2);
+      // again): publish tile kt + 1, then refill the stage of tile kt, whose reads are done.
       lds_read_barrier();
-      issue_tile<A16, true>(c, min(kt + S, KT - 1), la, lb);
+      issue_tile<A16, true>(c, min(kt + S, KT - 1), la);
     }
+    // weight fragments of step sigma + 3 (tile kt step 3, or tile kt + 1 step kk - 1), into the
+    // slot step sigma - 1 used
+    if constexpr (kk == 0)
+      load_b(c, kt, 3, p.bq[3]);
+    else
+      load_b(c, kt + 1, kk - 1, p.bq[kk - 1]);
     // LDS words of step sigma + 2 (tile kt step kk + 2, or tile kt + 1 step kk - 2)
     if (kk < 2)
-      read_step<A16>(c, la, lb, kk + 2, p.raw[kk & 1]);
+      read_step<A16>(c, la, kk + 2, p.raw[kk & 1]);
     else
-      read_step<A16>(c, na, nb, kk - 2, p.raw[kk & 1]);
-    // operands of step sigma + 1
-    convert_step<A16>(p.raw[(kk + 1) & 1], p.af[(kk + 1) & 1], p.bf[(kk + 1) & 1]);
+      read_step<A16>(c, na, kk - 2, p.raw[kk & 1]);
+    // activations of step sigma + 1
+    convert_step<A16>(p.raw[(kk + 1) & 1], p.af[(kk + 1) & 1]);
     // MFMAs of step sigma.  16-bit acts: fragments mt = 2 i (high bytes) and 2 i + 1 (low
     // bytes) of row block i; columns nt = 0 (weight codes) and 1 (rounding residues).  The low
     // bytes' residue products are left out: their sum is bounded (|lo'| <= 128) and completed
@@ -417,21 +441,22 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
     static_for<4>([&](auto mt) {
       static_for<kNT>([&](auto nt) {
         if constexpr (!(A16 && (decltype(mt)::value & 1) && decltype(nt)::value == 1))
-          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(p.af[kk & 1][mt], p.bf[kk & 1][nt], acc[mt][nt], 0, 0, 0);
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(p.af[kk & 1][mt], p.bq[kk][nt], acc[mt][nt], 0, 0, 0);
       });
     });
-    // issue order: the fragment reads early, then one MFMA and a few conversion instructions
-    // at a time
+    // issue order: the loads and fragment reads early, then one MFMA and a few conversion
+    // instructions at a time
     constexpr int kMfmas = A16 ? 6 : 4 * kNT;
     constexpr int kValu = A16 ? 4 : 2;  // conversion work per MFMA
     static_for<kMfmas>([&](auto i) {
       constexpr int ii = decltype(i)::value;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if constexpr (ii < 4 + kNT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if constexpr (ii < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if constexpr (ii < kNT) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       if constexpr (kk == 2) {
         // the stage's tile loads, spread over the step's MFMAs
-        constexpr int per = (C::kLoads + kMfmas - 1) / kMfmas;
-        constexpr int n = C::kLoads - ii * per < per ? (C::kLoads - ii * per > 0 ? C::kLoads - ii * per : 0) : per;
+        constexpr int per = (C::kLoadsA + kMfmas - 1) / kMfmas;
+        constexpr int n = C::kLoadsA - ii * per < per ? (C::kLoadsA - ii * per > 0 ? C::kLoadsA - ii * per : 0) : per;
         if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x002, kValu + (kk == 2 ? 4 : 0), 0);
@@ -448,9 +473,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // direct-to-LDS loads in flight (into other stages) cannot alias the fragment reads, and
   // does not make the reads wait for them.
   constexpr int S = C::kStages;
-  static_assert(S == 2, "two stages");
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[kTileA], sA1[kTileA];
-  __shared__ __attribute__((aligned(16))) uint8_t sB0[C::kTileB], sB1[C::kTileB];
+  static_assert(S == 2 || S == 3, "two or three stages");
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kTileA], sA1[kTileA], sA2[S == 3 ? kTileA : 16];
   __shared__ uint32_t fix_list[kFixCap];  // (row << 16 | column) inside the tile
   // The exact integer sums of each listed output, taken from the accumulators: 8-bit acts
   // S1 = sum (a - 128) w (int32); 16-bit acts X = sum (a - 32896) w and Y = sum (a - 32896) r.
@@ -461,7 +485,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   //   16-bit acts: [alpha | alpha * M | beta' | thr] x 128 columns.
   __shared__ double ctab[MODE == 0 ? 768 : 1];
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave & 1, wn = wave >> 1;  // 128-row half, 64-column quarter of the tile
   int tm, tn;
   tile_of(blockIdx.x, g.TM, g.TN, &tm, &tn);
@@ -475,16 +499,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   if (t == 0) fix_cnt = 0;
 
   // stage indices are compile-time constants everywhere (the k loop is unrolled by S)
-  auto stage_a = [&](auto st) -> uint8_t * { return st == 0 ? sA0 : sA1; };
-  auto stage_b = [&](auto st) -> uint8_t * { return st == 0 ? sB0 : sB1; };
+  auto stage_a = [&](auto st) -> uint8_t * { return st == 0 ? sA0 : (st == 1 ? sA1 : sA2); };
 
-  const MainCtx mc{act, btiles, M, K, m0, t, lane, wave, wm, wn};
+  const MainCtx mc{act, btiles + wn * (2 * kNT * 512), static_cast<uint32_t>(lane * 16), M, K, KT, m0, t, lane, wave, wm, wn};
 
   v16i acc[4][kNT];
   static_for<4>([&](auto i) { static_for<kNT>([&](auto j) { acc[i][j] = v16i{}; }); });
 
-  // Per-column constants: loads issued ahead of the operand prologue, LDS writes after it (so
-  // only these loads are waited for).
+  // Prologue: the weight fragments of steps 0..2 and both activation stages (assembly, like the
+  // loop's requests), then the per-column constants.  Those are ordinary loads issued last, so
+  // the compiler's wait for them (before the table writes below) also covers every operand
+  // request before them: the loop starts with nothing of the prologue in flight.
+  PipeRegs pr;
+  load_b(mc, 0, 0, pr.bq[0]);
+  load_b(mc, 0, 1, pr.bq[1]);
+  load_b(mc, 0, 2, pr.bq[2]);
+  static_for<S>([&](auto p) { issue_tile<A16, true>(mc, min(static_cast<int>(p), KT - 1), stage_a(p)); });
   double cv[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
   int64_t ccorr = 0, cmant = 0;
   const int ccol = A16 ? (t & 127) : (t & 255);
@@ -497,7 +527,6 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     ccorr = g.corr[cn];
     if (A16) cmant = g.mant[cn];
   }
-  static_for<S>([&](auto p) { issue_tile<A16, false>(mc, min(static_cast<int>(p), KT - 1), stage_a(p), stage_b(p)); });
   if (MODE == 0) {
     const double alpha = cv[0];
     // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
@@ -520,42 +549,31 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   }
 
   // k loop, unrolled by the stage count so every stage is a compile-time LDS object
-  PipeRegs pr;
   {
-    // tile 0 landed (the S - 1 later slots may stay in flight), its first steps read
-    wait_tiles<C::kLoads>(S - 1);
-    lds_read_barrier();  // also publishes the per-column constants written above
-    read_step<A16>(mc, sA0, sB0, 0, pr.raw[0]);
-    read_step<A16>(mc, sA0, sB0, 1, pr.raw[1]);
-    convert_step<A16>(pr.raw[0], pr.af[0], pr.bf[0]);
+    wait_vmcnt<0>();     // the prologue's requests (MODE 1 has no constants to wait for)
+    lds_read_barrier();  // tiles 0 .. S - 1 landed in every wave; also publishes the constants above
+    read_step<A16>(mc, sA0, 0, pr.raw[0]);
+    read_step<A16>(mc, sA0, 1, pr.raw[1]);
+    convert_step<A16>(pr.raw[0], pr.af[0]);
   }
   auto tile = [&](const int kt, auto sc) __attribute__((always_inline)) {
     constexpr int rs = decltype(sc)::value, ns = (rs + 1) % S;
-    k_tile<A16>(mc, kt, KT, stage_a(sc), stage_b(sc), stage_a(std::integral_constant<int, ns>{}),
-                stage_b(std::integral_constant<int, ns>{}), pr, acc);
+    k_tile<A16>(mc, kt, KT, stage_a(sc), stage_a(std::integral_constant<int, ns>{}), pr, acc);
   };
-  // 8-bit acts: tile 0 runs first on its own; it waits for the prologue's loads (the only ones
-  // the compiler knows of), so none of those is in flight in the loop.  (16-bit acts keep
-  // tile 0 in the loop: their registers do not allow the extra copy.)  The loop body is
-  // branch-free (whole tile pairs), so the compiler's wait counts for the fragment reads stay
-  // exact across iterations; an odd last tile runs after it.
-  if (!A16) {
-    tile(0, std::integral_constant<int, 0>{});
-    int kt0 = 1;
-    for (; kt0 + S <= KT; kt0 += S) {
-      tile(kt0, std::integral_constant<int, 1>{});
-      tile(kt0 + 1, std::integral_constant<int, 0>{});
-    }
-    if (kt0 < KT) tile(kt0, std::integral_constant<int, 1>{});
-  } else {
-    int kt0 = 0;
-    for (; kt0 + S <= KT; kt0 += S) {
-      tile(kt0, std::integral_constant<int, 0>{});
-      tile(kt0 + 1, std::integral_constant<int, 1>{});
-    }
-    if (kt0 < KT) tile(kt0, std::integral_constant<int, 0>{});
-  }
-  wait_vmcnt<0>();  // the tile loads issued from assembly have landed
+  // The loop body is S whole tiles (every stage a compile-time object, no branch inside); the
+  // last KT mod S tiles run after it.
+  int kt0 = 0;
+  for (; kt0 + S <= KT; kt0 += S) static_for<S>([&](auto j) { tile(kt0 + decltype(j)::value, j); });
+  static_for<S - 1>([&](auto j) {
+    if (kt0 + decltype(j)::value < KT) tile(kt0 + decltype(j)::value, j);
+  });
+  // Every request issued from assembly has landed.  The ring's registers pass through the wait:
+  // the weight loads of the steps past the end are never read, and without this use the
+  // compiler would hand their registers to other values while the loads can still write them.
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(pr.bq[0][0]), "+v"(pr.bq[0][1]), "+v"(pr.bq[1][0]), "+v"(pr.bq[1][1]), "+v"(pr.bq[2][0]),
+                 "+v"(pr.bq[2][1]), "+v"(pr.bq[3][0]), "+v"(pr.bq[3][1]));
+  static_assert(Cfg::kBRing == 4 && kNT == 2, "every ring slot passes through the final wait");
   // ---------------------------------------------------------------- epilogue
   // Straight from the accumulator registers: each lane requantises the 4-row strips of its
   // MFMA blocks (one column), then the 4 lanes of a quad transpose their strips (DPP quad

@@ -19,20 +19,22 @@ constexpr int kFixCap = 1024;
 
 // Tile storage of the GEMM weight operand (the "B" operand of the MFMA): int8 integer weights
 // (int4 codes and LPBQ code * block scale widened at prepare time).  A tile (nt, kt) covers 256
-// operand columns x 128 k (32 KiB) and is stored exactly as the GEMM keeps it in LDS, so the
-// kernel fills LDS with straight 16-byte direct-to-LDS copies: column c owns 128 B = eight 16-k
-// chunks, chunk s at 16 * (s ^ swz8(c)).
+// operand columns x 128 k (32 KiB) in MFMA fragment order: the 16 bytes of column c, depth
+// k .. k + 15 (k % 16 == 0) are lane 32 h + (c & 31) of the v_mfma_i32_32x32x32_i8 B fragment of
+// 32-k step s and 32-column block cb, with s = (k & 127) >> 5, h = (k >> 4) & 1, cb = c >> 5, and
+// the 64 lanes of one fragment are 1 KiB in a row, fragment (s, cb) at 1 KiB * (8 s + cb).  A wave
+// loads a whole fragment with one coalesced 16-byte-per-lane load straight into registers.
 // Element format of the decode GEMV stream: int8 codes, or int4 codes (two per byte).
 enum TileFormat : int { kTileI8 = 0, kTileI4 = 1 };
 
-// XOR swizzles that make the MFMA fragment reads bank-conflict free (32 consecutive rows or
-// columns reading the same logical chunk hit distinct banks for 8- or 16-lane LDS phases).
+// XOR swizzles that make the activation fragment reads from LDS bank-conflict free (32
+// consecutive rows reading the same logical chunk hit distinct banks for 8- or 16-lane LDS phases).
 __host__ __device__ inline int swz8(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
 __host__ __device__ inline int swz16(int row) { return row & 15; }
 
-// Byte offset of (operand column c, depth k) inside its tile.
+// Byte offset of (operand column c, depth k) inside its tile (fragment order, see above).
 __host__ __device__ inline int tile_off_i8(int c, int k) {
-  return c * 128 + 16 * (((k & 127) >> 4) ^ swz8(c)) + (k & 15);
+  return (((((k & 127) >> 5) * 8 + (c >> 5)) * 64 + ((k >> 4) & 1) * 32 + (c & 31)) << 4) + (k & 15);
 }
 
 // GEMV k-split: the 4 waves x 4 lanes of a workgroup that share a column take its 32-k groups
@@ -99,7 +101,9 @@ struct QmmDevice {
   double *margin_lo;      // 16-bit acts: bound of sum_k lo'_k r_k in output LSB (the GEMM and the int4-code
                           // GEMV form the high-byte residue sum exactly)
   int8_t *resid;    // 8-bit acts: rounding residues r[n][k] (fl32(w s32) = 2^E (w M + r)), [N][K],
-                    // read by the GEMM's exact fixup (|r| <= 64)
+                    // read by the GEMM's exact fixup (|r| <= 64): one contiguous row per listed
+                    // output, where the same weights in the fragment-ordered tiles are 256
+                    // scattered 16-byte pieces
   int32_t *bias_q;  // [Np] the descriptor's int32 bias (integer contracts)
   int64_t *corr_int; // [Np] activation-shift term of the exact integer dot product sum (a - zp) w_int
   // Per-group weights (exact integer GEMM): multipliers of the code and residue planes per

@@ -328,6 +328,10 @@ extern "C" qh_status qh_qmm_prepare(const qh_qmm_desc *d, qh_qmm_prepared **out)
       if (static_cast<double>(Wp) != wp) return fail(QH_STATUS_RUNTIME_ERROR, "internal: non-integer residue at n=%d", n);
       const int64_t r = Wp - static_cast<int64_t>(w) * M;
       if (r < -127 || r > 127) return fail(QH_STATUS_RUNTIME_ERROR, "internal: residue %lld out of int8", (long long)r);
+      // The GEMM's fixup of listed outputs beyond its list capacity recomputes r from w and M on
+      // the device as fl32(w M) - w M: the two must agree (they do unless w s32 overflows).
+      if (static_cast<int64_t>(static_cast<float>(w) * static_cast<float>(M)) - static_cast<int64_t>(w) * M != r)
+        return fail(QH_STATUS_INVALID_ARGUMENT, "weight_scale[%d]: the dequantised weights leave the float32 range", n);
       wint[static_cast<size_t>(n) * K + k] = static_cast<int8_t>(w);
       resid[static_cast<size_t>(n) * K + k] = static_cast<int8_t>(r);
       cq += w;
