@@ -1,11 +1,13 @@
 // Quantized GEMM on gfx950 i8 MFMA (v_mfma_i32_32x32x32_i8), bit-exact to the reference's
 // float-derived requantisation.
 //
-// Workgroup: 512 threads = 8 waves (two per SIMD) in a 2 x 4 grid over a 256 x 256 tile of
-// the i8 operand space (activation rows x weight-operand columns); each wave owns 4 x 2 MFMA
-// 32x32 blocks (128 rows x 64 columns).  Two waves per SIMD let one wave's LDS reads and
+// Workgroup: 512 threads = 8 waves (two per SIMD) side by side over a kBM x kBN = 128 x 512 tile
+// of the i8 operand space (activation rows x weight-operand columns); each wave owns 4 x 2 MFMA
+// 32x32 blocks (all 128 rows x 64 columns).  Two waves per SIMD let one wave's LDS reads and
 // conversions run under the other's MFMAs (a lone wave stalls its MFMAs on its own LDS reads).
-// K is consumed 128 deep per pipeline step.
+// The 128-row activation tile is shared by all eight waves, so each k step writes half the LDS
+// bytes of a 256 x 256 tile (whose every fragment row is read by four waves either way), and
+// each weight fragment is loaded by exactly one wave.  K is consumed 128 deep per pipeline step.
 //
 // Data movement: activation tiles go global -> LDS with direct-to-LDS loads
 // (global_load_lds_dwordx4), bypassing VGPRs, gathered into a swizzled layout by the per-lane
@@ -66,11 +68,12 @@ struct GemmArgs {
   double sA, sO;
 };
 
-constexpr int kTileA = 32768;  // A8: 256 rows x 128 B; A16: 128 rows x 256 B
+constexpr int kTileA = kBM * kBK;  // A8: kBM rows x 128 B; A16: kBM / 2 rows x 256 B
+constexpr int kWM = kBM / 128;     // waves along the tile's rows (each wave: 128 A8 rows x 64 operand columns)
 constexpr int kNT = 2;         // 32-column MFMA blocks per wave
 
 struct Cfg {
-  static constexpr int kTileB = 32768;  // 256 operand columns x 128 k, int8
+  static constexpr int kTileB = kBN * kBK;  // kBN operand columns x 128 k, int8
 #ifndef QH_GEMM_STAGES
 #define QH_GEMM_STAGES 2
 #endif
@@ -255,12 +258,13 @@ __device__ __forceinline__ void fixup_one(const GemmArgs &g, int m, int n, int l
 
 // Tile coordinates of this workgroup.  Workgroups are dispatched round-robin over the 8 XCDs
 // (each with its own L2); consecutive tile indices are given to one XCD and walked in groups
-// of 4 row tiles, so an XCD's concurrent tiles share activation rows and weight columns.
+// of 1024 / kBM row tiles, so an XCD's 32 concurrent tiles (8 row tiles x 4 column panels)
+// share activation rows and weight columns: 8 x 0.5 + 4 x 2 MB of operands at K = 4096.
 __device__ __forceinline__ void tile_of(int w, int TM, int TN, int *tm, int *tn) {
   const int T = TM * TN;
   int lin = w;
   if ((T & 7) == 0) lin = (w & 7) * (T >> 3) + (w >> 3);
-  constexpr int GM = 4;
+  constexpr int GM = 1024 / kBM;
   const int group = GM * TN;
   const int gid = lin / group, first = gid * GM;
   const int gm = TM - first < GM ? TM - first : GM;
@@ -314,7 +318,7 @@ __device__ __forceinline__ void issue_tile(const MainCtx &c, int kt, uint8_t *__
 // compiler's own counts would not see the DMA and would wait for requests issued later).  The
 // registers receive their data only after a covering wait_b().
 __device__ __forceinline__ void load_b(const MainCtx &c, int kt, int kk, v4i (&b)[kNT]) {
-  const uint8_t *p = c.bw + static_cast<size_t>(min(kt, c.KT - 1)) * Cfg::kTileB + kk * 8192;
+  const uint8_t *p = c.bw + static_cast<size_t>(min(kt, c.KT - 1)) * Cfg::kTileB + kk * (kBN / 32) * 1024;
   static_assert(kNT == 2, "two fragments per step");
   asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(b[0]) : "v"(c.boff), "s"(p));
   asm volatile("global_load_dwordx4 %0, %1, %2 offset:1024" : "=v"(b[1]) : "v"(c.boff), "s"(p));
@@ -481,12 +485,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   __shared__ int64_t fix_val[MODE == 0 ? (A16 ? 2 * kFixCap : kFixCap / 2) : 1];
   __shared__ int fix_cnt;
   // Per-column epilogue constants of the tile, filled while the first operand tiles load.
-  //   8-bit acts : [alpha | beta' | thr] x 256 columns;
-  //   16-bit acts: [alpha | alpha * M | beta' | thr] x 128 columns.
-  __shared__ double ctab[MODE == 0 ? 768 : 1];
+  //   8-bit acts : [alpha | beta' | thr] x kBN columns;
+  //   16-bit acts: [alpha | alpha * M | beta' | thr] x kBN / 2 columns.
+  constexpr int CB = A16 ? kBN / 2 : kBN;  // real output columns of the tile
+  __shared__ double ctab[MODE == 0 ? (A16 ? 4 : 3) * CB : 1];
 
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wm = wave & 1, wn = wave >> 1;  // 128-row half, 64-column quarter of the tile
+  const int wm = wave % kWM, wn = wave / kWM;  // the wave's 128 rows and 64 operand columns of the tile
   int tm, tn;
   tile_of(blockIdx.x, g.TM, g.TN, &tm, &tn);
   const int rows_real = A16 ? kBM / 2 : kBM;
@@ -517,7 +522,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   static_for<S>([&](auto p) { issue_tile<A16, true>(mc, min(static_cast<int>(p), KT - 1), stage_a(p)); });
   double cv[5] = {0.0, 0.0, 0.0, 0.0, 0.0};
   int64_t ccorr = 0, cmant = 0;
-  const int ccol = A16 ? (t & 127) : (t & 255);
+  static_assert(kBN <= kGemmThreads, "one thread per column loads the column constants");
+  const int ccol = t & (CB - 1);
   const int cn = n0 + ccol < g.N ? n0 + ccol : 0;
   if (MODE == 0) {
     cv[0] = g.alpha[cn];
@@ -532,19 +538,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     // zero-point correction folded into the offset: t = acc * alpha + (beta + corr * alpha)
     const double betap = fma(static_cast<double>(ccorr), alpha, cv[1]);
     const double corr_term = 2.0 * fabs(static_cast<double>(ccorr) * alpha);
-    if (!A16 && t < 256) {
+    if (!A16 && t < CB) {
       // |t - rint(t)| <= thr certifies the rounding; slack for |t| <= qmax + 2 folded in
       ctab[t] = alpha;
-      ctab[256 + t] = betap;
-      ctab[512 + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + static_cast<double>(g.out_qmax) + 2.0);
-    } else if (A16 && t < 128) {
+      ctab[CB + t] = betap;
+      ctab[2 * CB + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + static_cast<double>(g.out_qmax) + 2.0);
+    } else if (A16 && t < CB) {
       // t = Y * alpha + (X * alpha M + beta'); |X| <= K * 33024 * 127 bounds the float slack
       const double alpha_m = alpha * static_cast<double>(cmant);
       const double umax = fabs(alpha_m) * static_cast<double>(K) * (33024.0 * 127.0);
       ctab[t] = alpha;
-      ctab[128 + t] = alpha_m;
-      ctab[256 + t] = betap;
-      ctab[384 + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + umax + static_cast<double>(g.out_qmax) + 2.0);
+      ctab[CB + t] = alpha_m;
+      ctab[2 * CB + t] = betap;
+      ctab[3 * CB + t] = 0.5 - cv[2] - 0x1p-48 * (cv[3] + corr_term + umax + static_cast<double>(g.out_qmax) + 2.0);
     }
   }
 
@@ -635,7 +641,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   if (!A16) {
     static_for<kNT>([&](auto nt) {
       const int cl = wn * 64 + nt * 32 + (lane & 31);  // column inside the tile
-      const double alpha = ctab[cl], beta = ctab[256 + cl], thr = ctab[512 + cl];
+      const double alpha = ctab[cl], beta = ctab[CB + cl], thr = ctab[2 * CB + cl];
       static_for<4>([&](auto mt) {
         static_for<4>([&](auto jg) {
           const int R = wm * 128 + mt * 32 + 8 * jg + 4 * (lane >> 5);  // first of 4 rows
@@ -678,7 +684,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
     {
       constexpr int c = 0;  // one group of 32 real columns per wave
       const int cl = wn * 32 + (lane & 31);
-      const double alpha = ctab[cl], alpha_m = ctab[128 + cl], beta = ctab[256 + cl], thr = ctab[384 + cl];
+      const double alpha = ctab[cl], alpha_m = ctab[CB + cl], beta = ctab[2 * CB + cl], thr = ctab[3 * CB + cl];
       static_for<2>([&](auto mt) {
         static_for<4>([&](auto jg) {
           const int R = wm * 64 + mt * 32 + 8 * jg + 4 * (lane >> 5);

@@ -10,8 +10,8 @@ namespace qh {
 
 // GEMM workgroup tile in the i8 operand space: BM rows of the activation operand,
 // BN columns of the weight operand, BK bytes of K per pipeline stage.
-constexpr int kBM = 256;
-constexpr int kBN = 256;
+constexpr int kBM = 128;
+constexpr int kBN = 512;
 constexpr int kBK = 128;
 constexpr int kGemmThreads = 512;
 // Capacity of the per-workgroup list of outputs that need the exact fp64 fixup.
@@ -22,8 +22,8 @@ constexpr int kFixCap = 1024;
 // operand columns x 128 k (32 KiB) in MFMA fragment order: the 16 bytes of column c, depth
 // k .. k + 15 (k % 16 == 0) are lane 32 h + (c & 31) of the v_mfma_i32_32x32x32_i8 B fragment of
 // 32-k step s and 32-column block cb, with s = (k & 127) >> 5, h = (k >> 4) & 1, cb = c >> 5, and
-// the 64 lanes of one fragment are 1 KiB in a row, fragment (s, cb) at 1 KiB * (8 s + cb).  A wave
-// loads a whole fragment with one coalesced 16-byte-per-lane load straight into registers.
+// the 64 lanes of one fragment are 1 KiB in a row, fragment (s, cb) at 1 KiB * (kBN / 32 * s + cb).
+// A wave loads a whole fragment with one coalesced 16-byte-per-lane load straight into registers.
 // Element format of the decode GEMV stream: int8 codes, or int4 codes (two per byte).
 enum TileFormat : int { kTileI8 = 0, kTileI4 = 1 };
 
@@ -34,7 +34,7 @@ __host__ __device__ inline int swz16(int row) { return row & 15; }
 
 // Byte offset of (operand column c, depth k) inside its tile (fragment order, see above).
 __host__ __device__ inline int tile_off_i8(int c, int k) {
-  return (((((k & 127) >> 5) * 8 + (c >> 5)) * 64 + ((k >> 4) & 1) * 32 + (c & 31)) << 4) + (k & 15);
+  return (((((k & 127) >> 5) * (kBN / 32) + (c >> 5)) * 64 + ((k >> 4) & 1) * 32 + (c & 31)) << 4) + (k & 15);
 }
 
 // GEMV k-split: the 4 waves x 4 lanes of a workgroup that share a column take its 32-k groups
