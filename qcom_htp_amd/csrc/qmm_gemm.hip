@@ -740,49 +740,88 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   // oracle's dot product.  Marks beyond the list's capacity stay in the mark words and are
   // handled in later passes that form S1 and S2 from the operands (base 128 or 32768).
   const int KC = K / 16;
-  constexpr int P = 4;  // 16-byte K chunks per lane in flight
+  constexpr int P = A16 ? 2 : 4;  // 16-byte K chunks per lane in flight (16-bit acts: 48 bytes each)
   lds_read_barrier();   // listed outputs and overflow marks complete
   const int listed = fix_cnt;
   if (listed > 0) {
-    __syncthreads();  // every provisional output is stored before any is rewritten
     const int cnt = listed < kFixCap ? listed : kFixCap;
     const int abase_acc = A16 ? 32896 : 128;
-    for (int e = wave; e < cnt; e += kGemmThreads / 64) {
+    // Operands of one listed output: its column's constants and, per K round of 64 lanes x P
+    // chunks of 16 k, the activation row and the residue row (8-bit acts) or the residue column
+    // of the tiles (16-bit acts).  Chunks past K read chunk 0 and count as zero.
+    struct FixOps {
+      int m, n;
+      long long mant, csum, csum_r;
+      double alpha_e, beta, margin, absb;
+      uint4 av[P][A16 ? 2 : 1], rv[P];
+    };
+    auto fix_rows = [&](FixOps &f, int kc0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) {
+        const int kc = kc0 + lane + 64 * pp;
+        const int kk = kc < KC ? kc : 0;
+        if (!A16) {
+          f.av[pp][0] = reinterpret_cast<const uint4 *>(act + static_cast<size_t>(f.m) * K)[kk];
+          f.rv[pp] = reinterpret_cast<const uint4 *>(g.resid + static_cast<size_t>(f.n) * K)[kk];
+        } else {
+          const uint16_t *const arow = reinterpret_cast<const uint16_t *>(act) + static_cast<size_t>(f.m) * K;
+          f.rv[pp] = load_w16_raw(g, (f.n / 32) * 64 + 32 + (f.n % 32), kk * 16);
+          f.av[pp][0] = *reinterpret_cast<const uint4 *>(arow + kk * 16);
+          f.av[pp][A16 ? 1 : 0] = *reinterpret_cast<const uint4 *>(arow + kk * 16 + 8);
+        }
+      }
+    };
+    auto fix_load = [&](FixOps &f, int e) __attribute__((always_inline)) {
       const uint32_t v = __builtin_amdgcn_readfirstlane(fix_list[e]);  // uniform in the wave
-      const int m = m0 + static_cast<int>(v >> 16), n = n0 + static_cast<int>(v & 0xFFFFu);
-      // the column's constants are requested first, so their loads overlap the operand rows'.
-      // The index goes through a vector register: as wave-uniform values the compiler would
-      // move them to scalar registers at once, which waits for the loads before the rows issue.
-      int nv = n;
+      f.m = m0 + static_cast<int>(v >> 16);
+      f.n = n0 + static_cast<int>(v & 0xFFFFu);
+      // The index goes through a vector register: as wave-uniform values the compiler would move
+      // the constants to scalar registers at once, which waits for their loads before the rows issue.
+      int nv = f.n;
       asm volatile("" : "+v"(nv));
-      const long long mant_n = g.mant[nv], csum_n = g.colsum[nv], csum_r_n = g.colsum_r[nv];
-      const double alpha_e_n = g.alpha_e[nv], beta_n = g.beta[nv], margin_n = g.margin_exact[nv], absb_n = g.absb[nv];
+      f.mant = g.mant[nv];
+      f.csum = g.colsum[nv];
+      f.csum_r = g.colsum_r[nv];
+      f.alpha_e = g.alpha_e[nv];
+      f.beta = g.beta[nv];
+      f.margin = g.margin_exact[nv];
+      f.absb = g.absb[nv];
+      fix_rows(f, 0);
+    };
+    // This wave's first listed output is requested before the wait for the provisional stores,
+    // so the operand latency and the store drain overlap.
+    FixOps fo;
+    if (wave < cnt) fix_load(fo, wave);
+    __syncthreads();  // every provisional output is stored before any is rewritten
+    for (int e = wave; e < cnt; e += kGemmThreads / 64) {
+      if (e != wave) fix_load(fo, e);
+      const int m = fo.m, n = fo.n;
       long long S1, S2;
-      if (!A16) {
-        S1 = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int32_t *>(fix_val)[e]);
-        // S2 = sum_k (a_k - 128) r_k: 16 k per lane and chunk, 64 lanes x P chunks per round;
-        // chunks past K read chunk 0 and count as zero residues (no branch in the round)
-        const uint4 *const arow = reinterpret_cast<const uint4 *>(act + static_cast<size_t>(m) * K);
-        const uint4 *const rrow = reinterpret_cast<const uint4 *>(g.resid + static_cast<size_t>(n) * K);
-        int s2 = 0;  // |.| <= 128 * 64 * K < 2^31
-        for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
-          uint4 av[P], rv[P];
+      int s2 = 0;  // 8-bit acts: sum_k (a_k - 128) r_k; 16-bit: sum_k lo'_k r_k (|.| <= 128 * 64 * K < 2^31)
+      for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
+        if (kc0 > 0) fix_rows(fo, kc0);
 #pragma unroll
-          for (int pp = 0; pp < P; ++pp) {
-            const int kc = kc0 + lane + 64 * pp;
-            const int kk = kc < KC ? kc : 0;
-            av[pp] = arow[kk];
-            rv[pp] = rrow[kk];
-          }
-#pragma unroll
-          for (int pp = 0; pp < P; ++pp) {
-            const uint32_t keep = kc0 + lane + 64 * pp < KC ? 0xFFFFFFFFu : 0u;
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].x ^ 0x80808080u), static_cast<int>(rv[pp].x & keep), s2, false);
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].y ^ 0x80808080u), static_cast<int>(rv[pp].y & keep), s2, false);
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].z ^ 0x80808080u), static_cast<int>(rv[pp].z & keep), s2, false);
-            s2 = __builtin_amdgcn_sdot4(static_cast<int>(av[pp].w ^ 0x80808080u), static_cast<int>(rv[pp].w & keep), s2, false);
+        for (int pp = 0; pp < P; ++pp) {
+          const uint32_t keep = kc0 + lane + 64 * pp < KC ? 0xFFFFFFFFu : 0u;
+          const uint4 r = fo.rv[pp];
+          if (!A16) {
+            const uint4 a = fo.av[pp][0];
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(a.x ^ 0x80808080u), static_cast<int>(r.x & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(a.y ^ 0x80808080u), static_cast<int>(r.y & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(a.z ^ 0x80808080u), static_cast<int>(r.z & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(a.w ^ 0x80808080u), static_cast<int>(r.w & keep), s2, false);
+          } else {
+            // low activation bytes (a & 255) - 128 times the residue column
+            const uint4 a0 = fo.av[pp][0], a1 = fo.av[pp][A16 ? 1 : 0];
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(perm(a0.y, a0.x, 0x06040200u) ^ 0x80808080u), static_cast<int>(r.x & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(perm(a0.w, a0.z, 0x06040200u) ^ 0x80808080u), static_cast<int>(r.y & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(perm(a1.y, a1.x, 0x06040200u) ^ 0x80808080u), static_cast<int>(r.z & keep), s2, false);
+            s2 = __builtin_amdgcn_sdot4(static_cast<int>(perm(a1.w, a1.z, 0x06040200u) ^ 0x80808080u), static_cast<int>(r.w & keep), s2, false);
           }
         }
+      }
+      if (!A16) {
+        S1 = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int32_t *>(fix_val)[e]);
         S2 = wave_sum(s2);
       } else {
         const long long x = fix_val[2 * e], y = fix_val[2 * e + 1];
@@ -790,42 +829,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
              (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(x >> 32))) << 32);
         S2 = static_cast<long long>(static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(y)))) |
              (static_cast<long long>(__builtin_amdgcn_readfirstlane(static_cast<int>(y >> 32))) << 32);
-        // + sum_k lo'_k r_k: low activation bytes (a & 255) - 128 times the residue column of the
-        // weight tiles, 16 k per lane and chunk; chunks past K count as zero
-        const int cr = (n / 32) * 64 + 32 + (n % 32);
-        const uint16_t *const arow = reinterpret_cast<const uint16_t *>(act) + static_cast<size_t>(m) * K;
-        int s2l = 0;  // |.| <= 128 * 64 * K < 2^31
-        for (int kc0 = 0; kc0 < KC; kc0 += 64 * P) {
-          uint4 rv[P], av[P][2];
-#pragma unroll
-          for (int pp = 0; pp < P; ++pp) {
-            const int kc = kc0 + lane + 64 * pp;
-            const int k = (kc < KC ? kc : 0) * 16;
-            rv[pp] = load_w16_raw(g, cr, k);
-            av[pp][0] = *reinterpret_cast<const uint4 *>(arow + k);
-            av[pp][1] = *reinterpret_cast<const uint4 *>(arow + k + 8);
-          }
-#pragma unroll
-          for (int pp = 0; pp < P; ++pp) {
-            const uint32_t keep = kc0 + lane + 64 * pp < KC ? 0xFFFFFFFFu : 0u;
-            const uint4 a0 = av[pp][0], a1 = av[pp][1];
-            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a0.y, a0.x, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].x & keep), s2l, false);
-            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a0.w, a0.z, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].y & keep), s2l, false);
-            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a1.y, a1.x, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].z & keep), s2l, false);
-            s2l = __builtin_amdgcn_sdot4(static_cast<int>(perm(a1.w, a1.z, 0x06040200u) ^ 0x80808080u), static_cast<int>(rv[pp].w & keep), s2l, false);
-          }
-        }
-        S2 += wave_sum(s2l);
+        S2 += wave_sum(s2);
       }
       // |D| < 2^63; partial terms may wrap, so the sum is formed modulo 2^64
-      const unsigned long long M64 = static_cast<unsigned long long>(mant_n);
-      const unsigned long long sw = M64 * static_cast<unsigned long long>(csum_n) + static_cast<unsigned long long>(csum_r_n);
+      const unsigned long long M64 = static_cast<unsigned long long>(fo.mant);
+      const unsigned long long sw = M64 * static_cast<unsigned long long>(fo.csum) + static_cast<unsigned long long>(fo.csum_r);
       const unsigned long long Du = M64 * static_cast<unsigned long long>(S1) + static_cast<unsigned long long>(S2) +
                                     static_cast<unsigned long long>(static_cast<long long>(abase_acc - g.act_zp)) * sw;
-      const double u = static_cast<double>(static_cast<long long>(Du)) * alpha_e_n;
-      const double tv = u + beta_n;
+      const double u = static_cast<double>(static_cast<long long>(Du)) * fo.alpha_e;
+      const double tv = u + fo.beta;
       const double rd = rint(tv);
-      const double slack = margin_n + 0x1p-48 * (fabs(u) + fabs(tv) + absb_n);
+      const double slack = fo.margin + 0x1p-48 * (fabs(u) + fabs(tv) + fo.absb);
       if (fabs(tv - rd) > 0.5 - slack) {
         fixup_one<A16>(g, m, n, lane);
       } else if (lane == 0) {
