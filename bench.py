@@ -301,6 +301,79 @@ def gdn_prefill_workload(B: int, T: int, H: int, steps: int, warmup: int, precis
             "stage_b_tflops_alg": flops_b / (ev_b * 1e-3) / 1e12, "oc_vs_fp64_worst_of_2_sequences": worst}
 
 
+def graph_chain_workload(name: str, reps: int, chain: int = 8):
+    """The reference's own CHAIN graph of family `name` at M = K = N = 256: its closed-form
+    operands and integer contract (qcom_htp_amd.cases.graph_case; gen_quant_chain.py:253-329,
+    971-996), `chain` dependent matmuls per graph run.  `reps` graph runs are captured in one HIP
+    graph and replayed; after the timed region the output is checked against the reference step
+    applied `chain` times."""
+    import numpy as np
+    import torch
+
+    from oracle import qmm as oq  # the checker
+    from qcom_htp_amd import cases
+    from qcom_htp_amd.qmm import QuantMatmul, graph_contract
+
+    dev = torch.device("cuda", 0)
+    gc = cases.graph_case(name)
+    op = QuantMatmul.from_graph_case(gc, device=dev)
+    contract, d = graph_contract(gc)
+    act = torch.from_numpy(gc.activation).to(dev)
+    out = torch.empty((256, 256), dtype=op.out_dtype, device=dev)
+    scr = torch.empty_like(out)
+    op.chain(act, chain, contract, d, out=out, scratch=scr)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            op.chain(act, chain, contract, d, out=out, scratch=scr)
+    wall, ev = time_kernel(lambda i: graph.replay(), 3, 1)
+    cur = gc.activation
+    for _ in range(chain):
+        cur = oq.reference_step(gc.act_bits, gc.weight_bits, gc.out_bits, cur, gc.weight_compute_kn, gc.bias_q,
+                                contract=gc.contract, family_name=gc.kernel_family)
+    bad = int((out.cpu().numpy().astype(np.int64) != cur.astype(np.int64)).sum())
+    if bad:
+        raise RuntimeError(f"graph chain {name}: {bad} outputs differ from the reference step applied {chain} times")
+    op.close()
+    us = ev * 1e3 / reps
+    return {"family": name, "m": 256, "k": 256, "n": 256, "chain": chain, "contract": f"{contract}/{d}",
+            "us_per_chain": us, "us_per_matmul": us / chain, "wall_us_per_chain": wall * 1e3 / reps,
+            "parity_outputs_checked": int(out.numel()), "parity_mismatches": bad,
+            "what": "the reference's CHAIN graph operands and contract, graph-replayed"}
+
+
+def gdn_u16_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
+    """The GdnSolve op's u16 I/O contract at C x heads: A quantised with the reference gate's
+    parameters (sA = max|A| / 32767, zero points 32768, sT = 2 / 32767,
+    scripts/gdn_solve_br_probe.py:59-60), T returned as u16 codes; oc of the dequantised T against
+    the float64 inverse of the dequantised A (scripts/gdn_solve_oc_check.py:28-31)."""
+    import numpy as np
+    import torch
+
+    from oracle import gdn as og  # the checker
+    from qcom_htp_amd.gdn import GdnSolve
+
+    k, beta, gc = og.config4_inputs(heads=heads, C=C, seed=4)
+    A = og.build_A(k, beta, gc)
+    sA = float(np.float32(max(np.abs(A).max() / 32767.0, 1e-12)))
+    sT = float(np.float32(2.0 / 32767.0))
+    codes = np.clip(np.rint(A / sA) + 32768, 0, 65535).astype(np.uint16)
+    dev = torch.device("cuda", 0)
+    a = torch.from_numpy(codes.view(np.int16)).to(dev).view(torch.uint16)
+    out = torch.empty_like(a)
+    wall, ev = time_kernel(lambda i: GdnSolve(a, 32768, sA, 32768, sT, precision=precision, out=out), steps, warmup)
+    Ad = (codes.astype(np.int64) - 32768) * sA
+    Td = (out.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.int64) - 32768) * sT
+    err = og.oc(Td, og.inverse_fp64(Ad))
+    if not err <= og.GATE_BF16:
+        raise RuntimeError(f"GDN u16 C={C}: oc {err:.3e} > {og.GATE_BF16}")
+    flops = (2.0 / 3.0) * C ** 3 * heads
+    return {"heads": heads, "C": C, "precision": "fp32" if precision == 0 else "bf16", "ms": ev, "wall_ms": wall,
+            "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12, "oc_vs_fp64": err,
+            "sA": sA, "sT": sT, "zp": 32768}
+
+
 def cpu_baseline(case, gdn_A):
     """The oracle (numpy/LAPACK/torch restatement of the reference's CPU path) on the host cores
     of this job: one warm-up, then the median of 5 runs per shape (3 for the slowest)."""
@@ -365,6 +438,14 @@ def cpu_baseline(case, gdn_A):
         gg = torch.nn.functional.logsigmoid(torch.from_numpy(rng.standard_normal((n, C))) + 3.0)
         t = med(lambda: og.chunk_stage_a_torch(kk, vv, gg, bb), reps=3)
         shapes[f"gdn_chunk_uw_c{C}_torch"] = {"s": t, "chunk_heads": n, "chunk_heads_per_s": n / t}
+    # the whole chunked prefill (stage A + the chunk recurrence, scripts/gdn_ref_kernel.py:104-131)
+    # in torch float64 on 8 of the 256 (batch, head) sequences of B=8, T=4096, H=32
+    ns, T = 8, 4096
+    qq, kk, vv = (torch.from_numpy(rng.standard_normal((ns, T, 128))) for _ in range(3))
+    gg = torch.nn.functional.logsigmoid(torch.from_numpy(rng.standard_normal((ns, T))) + 3.0)
+    bb = torch.sigmoid(torch.from_numpy(rng.standard_normal((ns, T))))
+    t = med(lambda: og.gdn_prefill_torch(qq, kk, vv, gg, bb, 64), reps=3)
+    shapes["gdn_prefill_c64_torch"] = {"s": t, "sequences": ns, "tokens": ns * T, "tokens_per_s": ns * T / t}
     return {
         "value": value,
         "unit": "TOPS",
@@ -485,6 +566,10 @@ def main() -> int:
         for prec in (0, 1):
             jobs.append((f"gdn_prefill_c64_{'fp32' if prec == 0 else 'bf16'}",
                          lambda prec=prec: gdn_prefill_workload(8, 4096, 32, 10, 2, prec)))
+        for prec in (0, 1):
+            jobs.append((f"gdn_u16_c256_h32_{'fp32' if prec == 0 else 'bf16'}", lambda prec=prec: gdn_u16_workload(32, 256, 50, 5, prec)))
+        for name in ("u8i8", "w4a8_per_channel", "w4a8_lpbq", "w8a16", "w4a16_per_channel", "w4a16_lpbq", "w16a16"):
+            jobs.append((f"graph_chain8_256_{name}", lambda name=name: graph_chain_workload(name, 50)))
         jobs.append(("lpbq_expand_4096x14336", lambda: lpbq_expand_workload(4096, 14336, 20, 3)))
         jobs.append(("vendor_int8_gemm_4096", lambda: vendor_int8_gemm_workload(M, K, N, 20, 5)))
         jobs.append(("vendor_copy_gemv_bytes", lambda: stream_copy_workload(30_410_000, 200, 10)))

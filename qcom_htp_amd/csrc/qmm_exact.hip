@@ -63,16 +63,16 @@ __device__ __forceinline__ void store_out(const ExactArgs &g, size_t idx, int v)
 }
 
 // The reference's integer contracts on the exact accumulator D = sum_k (a - zp) w.
-__device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, int n) {
+// bias: bias_q[n] (0 without a bias operand), read once per column before the k loop.
+__device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, long long bias) {
   const long long qmax = g.out_qmax;
   switch (g.contract) {
     case QH_CONTRACT_CLIP_I32: {  // int32 arithmetic of the reference (wraps modulo 2^32)
-      const long long b = g.bias_q ? g.bias_q[n] : 0;
-      const int v = static_cast<int>(static_cast<unsigned int>(static_cast<unsigned long long>(D + b)));
+      const int v = static_cast<int>(static_cast<unsigned int>(static_cast<unsigned long long>(D + bias)));
       return v < 0 ? 0 : (v > qmax ? static_cast<int>(qmax) : v);
     }
     case QH_CONTRACT_CLIP_I64: {
-      const long long v = D + (g.bias_q ? g.bias_q[n] : 0);
+      const long long v = D + bias;
       return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
     }
     case QH_CONTRACT_FLOOR256_DIV_RINT:
@@ -94,7 +94,7 @@ __device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, i
       const uint32_t e = (pk >> 10) & 31u, f = pk & 1023u;
       const double mag = e == 0 ? ldexp(static_cast<double>(f), -24) : ldexp(static_cast<double>(1024u + f), static_cast<int>(e) - 25);
       const double s = (pk & 0x8000u) ? -mag : mag;
-      const long long drain = D + (g.bias_q ? g.bias_q[n] : 0);
+      const long long drain = D + bias;
       const long long v = static_cast<long long>(trunc(static_cast<double>(drain) * s / 512.0)) + (pk >> 23);
       return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
     }
@@ -159,7 +159,7 @@ __device__ __forceinline__ void load_step(const ExactArgs &g, int mrow, int ncol
 }
 
 template <bool A16, int MODE>
-__global__ __launch_bounds__(kExThreads) void qmm_exact_kernel(const ExactArgs g) {
+__global__ __launch_bounds__(kExThreads, 2) void qmm_exact_kernel(const ExactArgs g) {
   constexpr int D = A16 ? 2 : 1;  // activation digits
   __shared__ uint32_t fix_list[MODE == 0 ? kExFixCap : 1];
   __shared__ int fix_cnt;
@@ -182,69 +182,10 @@ __global__ __launch_bounds__(kExThreads) void qmm_exact_kernel(const ExactArgs g
     one[d] = v16i{};
   }
   const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-  const int steps = g.K / 32;
-  Frag<A16> cur, nxt;
-  load_step<A16>(g, mrow, ncol, kq, cur);
-  for (int s = 0; s < steps; ++s) {
-    if (s + 1 < steps) load_step<A16>(g, mrow, ncol, 32 * (s + 1) + kq, nxt);
-    v4i af[D];
-    if (!A16) {
-      const uint4 v = cur.a[0];
-      af[0] = v4i{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
-                  static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
-    } else {
-      uint4 v0 = cur.a[0], v1 = cur.a[D - 1];
-      v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
-      v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
-      // a - 32768 = 256 hi + lo' + 128 with hi = high byte ^ 0x80, lo' = low byte ^ 0x80
-      af[0] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x07050301u)), static_cast<int>(perm(v0.w, v0.z, 0x07050301u)),
-                  static_cast<int>(perm(v1.y, v1.x, 0x07050301u)), static_cast<int>(perm(v1.w, v1.z, 0x07050301u))};
-      af[D - 1] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x06040200u)), static_cast<int>(perm(v0.w, v0.z, 0x06040200u)),
-                      static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
-    }
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        if (p >= g.nplanes) break;
-        const uint4 b = cur.b[p];
-        acc[p][d] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-            af[d], v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)},
-            acc[p][d], 0, 0, 0);
-      }
-      if (g.ones) one[d] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[d], ones, one[d], 0, 0, 0);
-    }
-    // every 64 k (and after the last step): int32 sums into the int64 accumulators
-    if ((s & 1) || s + 1 == steps) {
-      const int grp = (32 * s) >> g.gshift;
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        if (p >= g.nplanes) break;
-        const long long mlt = MODE == 0 ? g.mult[(static_cast<size_t>(p) * g.G + grp) * g.Np + ncol] : g.cm[p];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int v = A16 ? 256 * acc[p][0][j] + acc[p][D - 1][j] : acc[p][0][j];
-          acc64[j] += static_cast<long long>(v) * mlt;
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d) acc[p][d] = v16i{};
-      }
-      if (g.ones) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int v = A16 ? 256 * one[0][j] + one[D - 1][j] : one[0][j];
-          acc64[j] += static_cast<long long>(v) * g.ones;
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d) one[d] = v16i{};
-      }
-    }
-    if (s + 1 < steps) cur = nxt;
-  }
-
-  // ---- epilogue: lane holds rows m0 + 8 (j / 4) + 4 (lane / 32) + j % 4 of column ncol
-  const bool col_ok = ncol < g.N;
+  // The epilogue's per-column constants are requested before the k loop, so their latency
+  // overlaps the operand loads instead of following the products.
   const long long corr = g.corr[ncol];
+  const long long bq = MODE == 2 && g.bias_q ? g.bias_q[ncol] : 0;
   double alpha = 0.0, beta = 0.0, mex = 0.0, absb = 0.0;
   if (MODE == 0) {
     alpha = g.alpha_e[ncol];
@@ -252,6 +193,85 @@ __global__ __launch_bounds__(kExThreads) void qmm_exact_kernel(const ExactArgs g
     mex = g.margin_exact[ncol];
     absb = g.absb[ncol];
   }
+  const int steps = g.K / 32;
+  // Loads go out a batch of NB 32-k steps at a time, one batch ahead of the products: a short K
+  // (the reference's 256^3 graphs) then takes a few memory round trips instead of one per step.
+  // Slots past the last step reload it (unused), so every batch issues the same loads.
+  constexpr int NB = A16 ? 2 : 4;
+  const int nbatch = (steps + NB - 1) / NB;
+  Frag<A16> cur[NB], nxt[NB];
+  auto load_batch = [&](int b, Frag<A16>(&f)[NB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) load_step<A16>(g, mrow, ncol, 32 * min(b * NB + i, steps - 1) + kq, f[i]);
+  };
+  load_batch(0, cur);
+  for (int bt = 0; bt < nbatch; ++bt) {
+    if (bt + 1 < nbatch) load_batch(bt + 1, nxt);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int s = bt * NB + i;
+      if (s >= steps) break;  // wave-uniform
+      v4i af[D];
+      if (!A16) {
+        const uint4 v = cur[i].a[0];
+        af[0] = v4i{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
+                    static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
+      } else {
+        uint4 v0 = cur[i].a[0], v1 = cur[i].a[D - 1];
+        v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
+        v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
+        // a - 32768 = 256 hi + lo' + 128 with hi = high byte ^ 0x80, lo' = low byte ^ 0x80
+        af[0] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x07050301u)), static_cast<int>(perm(v0.w, v0.z, 0x07050301u)),
+                    static_cast<int>(perm(v1.y, v1.x, 0x07050301u)), static_cast<int>(perm(v1.w, v1.z, 0x07050301u))};
+        af[D - 1] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x06040200u)), static_cast<int>(perm(v0.w, v0.z, 0x06040200u)),
+                        static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
+      }
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if (p >= g.nplanes) break;
+          const uint4 b = cur[i].b[p];
+          acc[p][d] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+              af[d], v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)},
+              acc[p][d], 0, 0, 0);
+        }
+        if (g.ones) one[d] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[d], ones, one[d], 0, 0, 0);
+      }
+      // every 64 k (and after the last step): int32 sums into the int64 accumulators
+      if ((s & 1) || s + 1 == steps) {
+        const int grp = (32 * s) >> g.gshift;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if (p >= g.nplanes) break;
+          const long long mlt = MODE == 0 ? g.mult[(static_cast<size_t>(p) * g.G + grp) * g.Np + ncol] : g.cm[p];
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int v = A16 ? 256 * acc[p][0][j] + acc[p][D - 1][j] : acc[p][0][j];
+            acc64[j] += static_cast<long long>(v) * mlt;
+          }
+#pragma unroll
+          for (int d = 0; d < D; ++d) acc[p][d] = v16i{};
+        }
+        if (g.ones) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int v = A16 ? 256 * one[0][j] + one[D - 1][j] : one[0][j];
+            acc64[j] += static_cast<long long>(v) * g.ones;
+          }
+#pragma unroll
+          for (int d = 0; d < D; ++d) one[d] = v16i{};
+        }
+      }
+    }
+    if (bt + 1 < nbatch) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) cur[i] = nxt[i];
+    }
+  }
+
+  // ---- epilogue: lane holds rows m0 + 8 (j / 4) + 4 (lane / 32) + j % 4 of column ncol
+  const bool col_ok = ncol < g.N;
   __syncthreads();  // fix_cnt initialised
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -262,7 +282,7 @@ __global__ __launch_bounds__(kExThreads) void qmm_exact_kernel(const ExactArgs g
     if (MODE == 1) {
       static_cast<long long *>(g.out)[idx] = Dv;
     } else if (MODE == 2) {
-      store_out(g, idx, apply_contract(g, Dv, ncol));
+      store_out(g, idx, apply_contract(g, Dv, bq));
     } else {
       const double u = static_cast<double>(Dv) * alpha;
       const double tv = u + beta;
