@@ -301,6 +301,14 @@ def gdn_prefill_workload(B: int, T: int, H: int, steps: int, warmup: int, precis
             "stage_b_tflops_alg": flops_b / (ev_b * 1e-3) / 1e12, "oc_vs_fp64_worst_of_2_sequences": worst}
 
 
+# The reference's custom-op CHAIN=8 graphs at 256^3 on the Hexagon v75 HTP: (kernel "main" cycles,
+# graph timeline cycles) per graph run, example/qnn_matmul_profile/alignment_e2e_256_report.md:43-46,
+# at the 1.594 GHz TURBO clock of example/gdn_native/baremetal/src/gdnbm_test.c:84.
+REFERENCE_CHAIN8_CYCLES = {"u8i8": (10891, 36342), "w4a8_per_channel": (10025, 38644),
+                           "w8a16": (30871, 80217), "w4a16_per_channel": (31419, 77854)}
+REFERENCE_CLOCK_GHZ = 1.594
+
+
 def graph_chain_workload(name: str, reps: int, chain: int = 8):
     """The reference's own CHAIN graph of family `name` at M = K = N = 256: its closed-form
     operands and integer contract (qcom_htp_amd.cases.graph_case; gen_quant_chain.py:253-329,
@@ -337,8 +345,14 @@ def graph_chain_workload(name: str, reps: int, chain: int = 8):
         raise RuntimeError(f"graph chain {name}: {bad} outputs differ from the reference step applied {chain} times")
     op.close()
     us = ev * 1e3 / reps
+    ref = {}
+    if name in REFERENCE_CHAIN8_CYCLES and chain == 8:
+        main, timeline = REFERENCE_CHAIN8_CYCLES[name]
+        ref = {"reference_main_us": main / REFERENCE_CLOCK_GHZ / 1e3,
+               "reference_timeline_us": timeline / REFERENCE_CLOCK_GHZ / 1e3,
+               "speedup_vs_reference_timeline": timeline / REFERENCE_CLOCK_GHZ / 1e3 / us}
     return {"family": name, "m": 256, "k": 256, "n": 256, "chain": chain, "contract": f"{contract}/{d}",
-            "us_per_chain": us, "us_per_matmul": us / chain, "wall_us_per_chain": wall * 1e3 / reps,
+            **ref, "us_per_chain": us, "us_per_matmul": us / chain, "wall_us_per_chain": wall * 1e3 / reps,
             "parity_outputs_checked": int(out.numel()), "parity_mismatches": bad,
             "what": "the reference's CHAIN graph operands and contract, graph-replayed"}
 

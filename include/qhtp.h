@@ -180,7 +180,9 @@ qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const voi
  * Needs K == N and act_bits == out_bits when chain > 1.  Each step is qh_qmm_run
  * (contract = QH_CONTRACT_NONE) or qh_qmm_run_contract(contract, divisor).  Intermediate results
  * alternate between out_dev and scratch_dev (the op's scratch operand: M x N output elements;
- * NULL allowed when chain == 1), so the last one lands in out_dev.  act_dev is only read. */
+ * NULL allowed when chain == 1), so the last one lands in out_dev.  act_dev is only read.
+ * An integer-contract chain with K == N <= 256 runs every step in one launch, with the
+ * intermediate results on chip: scratch_dev is then required but left untouched. */
 qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t chain, const void *act_dev,
                            void *out_dev, void *scratch_dev, uint32_t contract, uint32_t divisor, void *stream);
 

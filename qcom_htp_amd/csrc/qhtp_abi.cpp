@@ -94,6 +94,23 @@ qh_status qh_qmm_accumulate(const qh_qmm_prepared *prep, uint32_t m, const void 
   return launch_qmm_accumulate(prep, static_cast<int>(m), act_dev, acc_dev, static_cast<hipStream_t>(stream));
 }
 
+namespace {
+
+// Validates a contract and its divisor; *param = the value the kernels take.
+qh_status contract_param(const char *fn, uint32_t contract, uint32_t divisor, uint32_t *param) {
+  if (contract > QH_CONTRACT_U8_DRAIN) return fail(QH_STATUS_UNSUPPORTED, "%s: unknown contract %u", fn, contract);
+  const bool divides = contract == QH_CONTRACT_DIV_RINT || contract == QH_CONTRACT_FLOOR256_DIV_RINT ||
+                       contract == QH_CONTRACT_ROUND_DIV;
+  if (divides && (divisor == 0 || divisor > (1u << 30)))
+    return fail(QH_STATUS_INVALID_ARGUMENT, "%s: divisor %u must be in [1, 2^30]", fn, divisor);
+  if (contract == QH_CONTRACT_U8_DRAIN && ((divisor >> 10) & 31u) == 31u)
+    return fail(QH_STATUS_INVALID_ARGUMENT, "%s: drain scale 0x%04x is not a finite half", fn, divisor & 0xFFFFu);
+  *param = divides || contract == QH_CONTRACT_U8_DRAIN ? divisor : 1u;
+  return QH_STATUS_OK;
+}
+
+}  // namespace
+
 qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const void *act_dev, void *out_dev,
                               uint32_t contract, uint32_t divisor, void *stream) {
   if (prep == nullptr) return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: prepared handle is NULL");
@@ -102,16 +119,9 @@ qh_status qh_qmm_run_contract(const qh_qmm_prepared *prep, uint32_t m, const voi
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: NULL buffer");
   if (reinterpret_cast<uintptr_t>(act_dev) % 16)
     return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: activation must be 16-byte aligned");
-  if (contract > QH_CONTRACT_U8_DRAIN)
-    return fail(QH_STATUS_UNSUPPORTED, "qh_qmm_run_contract: unknown contract %u", contract);
-  const bool divides = contract == QH_CONTRACT_DIV_RINT || contract == QH_CONTRACT_FLOOR256_DIV_RINT ||
-                       contract == QH_CONTRACT_ROUND_DIV;
-  if (divides && (divisor == 0 || divisor > (1u << 30)))
-    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: divisor %u must be in [1, 2^30]", divisor);
-  if (contract == QH_CONTRACT_U8_DRAIN && ((divisor >> 10) & 31u) == 31u)
-    return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_contract: drain scale 0x%04x is not a finite half",
-                divisor & 0xFFFFu);
-  const uint32_t param = divides || contract == QH_CONTRACT_U8_DRAIN ? divisor : 1u;
+  uint32_t param = 1;
+  const qh_status st = contract_param("qh_qmm_run_contract", contract, divisor, &param);
+  if (st != QH_STATUS_OK) return st;
   return launch_qmm_exact(prep, static_cast<int>(m), act_dev, out_dev, 2, static_cast<int>(contract),
                           static_cast<int>(param), static_cast<hipStream_t>(stream));
 }
@@ -136,6 +146,17 @@ qh_status qh_qmm_run_chain(const qh_qmm_prepared *prep, uint32_t m, uint32_t cha
     auto overlap = [](uintptr_t p, uintptr_t np, uintptr_t q, uintptr_t nq) { return p < q + nq && q < p + np; };
     if (overlap(a, na, o, no) || overlap(a, na, s, no) || overlap(o, no, s, no))
       return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: act, out and scratch ranges must not overlap");
+  }
+  if (chain > 1 && contract != QH_CONTRACT_NONE && chain_fusable(prep)) {
+    // every step in one launch: the intermediate activations stay on chip (scratch unused)
+    if (m == 0 || m > (1u << 22)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "qh_qmm_run_chain: bad M=%u", m);
+    if (reinterpret_cast<uintptr_t>(act_dev) % 16)
+      return fail(QH_STATUS_INVALID_ARGUMENT, "qh_qmm_run_chain: activation must be 16-byte aligned");
+    uint32_t param = 1;
+    const qh_status st = contract_param("qh_qmm_run_chain", contract, divisor, &param);
+    if (st != QH_STATUS_OK) return st;
+    return launch_qmm_chain(prep, static_cast<int>(m), static_cast<int>(chain), act_dev, out_dev,
+                            static_cast<int>(contract), static_cast<int>(param), static_cast<hipStream_t>(stream));
   }
   const void *src = act_dev;
   for (uint32_t i = 0; i < chain; ++i) {

@@ -64,40 +64,44 @@ __device__ __forceinline__ void store_out(const ExactArgs &g, size_t idx, int v)
 
 // The reference's integer contracts on the exact accumulator D = sum_k (a - zp) w.
 // bias: bias_q[n] (0 without a bias operand), read once per column before the k loop.
-__device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, long long bias) {
+template <int CT>
+__device__ __forceinline__ int contract_ct(const ExactArgs &g, long long D, long long bias) {
   const long long qmax = g.out_qmax;
+  if constexpr (CT == QH_CONTRACT_CLIP_I32) {  // int32 arithmetic of the reference (wraps modulo 2^32)
+    const int v = static_cast<int>(static_cast<unsigned int>(static_cast<unsigned long long>(D + bias)));
+    return v < 0 ? 0 : (v > qmax ? static_cast<int>(qmax) : v);
+  } else if constexpr (CT == QH_CONTRACT_CLIP_I64) {
+    const long long v = D + bias;
+    return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
+  } else if constexpr (CT == QH_CONTRACT_FLOOR256_DIV_RINT || CT == QH_CONTRACT_DIV_RINT) {
+    if (CT == QH_CONTRACT_FLOOR256_DIV_RINT) D = (D >> 8) * 256;  // floor division (shift rounds to -inf)
+    const double y = static_cast<double>(D) / static_cast<double>(g.divisor);
+    const double o = rint(y + static_cast<double>(g.out_zp));
+    return static_cast<int>(fmin(fmax(o, 0.0), static_cast<double>(qmax)));
+  } else if constexpr (CT == QH_CONTRACT_ROUND_DIV) {
+    const long long d = g.divisor, h = d / 2;
+    const long long q = D >= 0 ? (D + h) / d : -((-D + h) / d);
+    const long long v = q + g.out_zp;
+    return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
+  } else {  // QH_CONTRACT_U8_DRAIN: (acc + bias) * s / 512 in float64, truncated, + b >> 7
+    const uint32_t pk = static_cast<uint32_t>(g.divisor);
+    const uint32_t e = (pk >> 10) & 31u, f = pk & 1023u;
+    const double mag = e == 0 ? ldexp(static_cast<double>(f), -24) : ldexp(static_cast<double>(1024u + f), static_cast<int>(e) - 25);
+    const double s = (pk & 0x8000u) ? -mag : mag;
+    const long long drain = D + bias;
+    const long long v = static_cast<long long>(trunc(static_cast<double>(drain) * s / 512.0)) + (pk >> 23);
+    return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
+  }
+}
+
+__device__ __forceinline__ int apply_contract(const ExactArgs &g, long long D, long long bias) {
   switch (g.contract) {
-    case QH_CONTRACT_CLIP_I32: {  // int32 arithmetic of the reference (wraps modulo 2^32)
-      const int v = static_cast<int>(static_cast<unsigned int>(static_cast<unsigned long long>(D + bias)));
-      return v < 0 ? 0 : (v > qmax ? static_cast<int>(qmax) : v);
-    }
-    case QH_CONTRACT_CLIP_I64: {
-      const long long v = D + bias;
-      return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
-    }
-    case QH_CONTRACT_FLOOR256_DIV_RINT:
-      D = (D >> 8) * 256;  // floor division (arithmetic shift rounds toward -inf)
-      [[fallthrough]];
-    case QH_CONTRACT_DIV_RINT: {
-      const double y = static_cast<double>(D) / static_cast<double>(g.divisor);
-      const double o = rint(y + static_cast<double>(g.out_zp));
-      return static_cast<int>(fmin(fmax(o, 0.0), static_cast<double>(qmax)));
-    }
-    case QH_CONTRACT_ROUND_DIV: {
-      const long long d = g.divisor, h = d / 2;
-      const long long q = D >= 0 ? (D + h) / d : -((-D + h) / d);
-      const long long v = q + g.out_zp;
-      return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
-    }
-    case QH_CONTRACT_U8_DRAIN: {  // (acc + bias) * s / 512 in float64, truncated, + b >> 7
-      const uint32_t pk = static_cast<uint32_t>(g.divisor);
-      const uint32_t e = (pk >> 10) & 31u, f = pk & 1023u;
-      const double mag = e == 0 ? ldexp(static_cast<double>(f), -24) : ldexp(static_cast<double>(1024u + f), static_cast<int>(e) - 25);
-      const double s = (pk & 0x8000u) ? -mag : mag;
-      const long long drain = D + bias;
-      const long long v = static_cast<long long>(trunc(static_cast<double>(drain) * s / 512.0)) + (pk >> 23);
-      return static_cast<int>(v < 0 ? 0 : (v > qmax ? qmax : v));
-    }
+    case QH_CONTRACT_CLIP_I32: return contract_ct<QH_CONTRACT_CLIP_I32>(g, D, bias);
+    case QH_CONTRACT_CLIP_I64: return contract_ct<QH_CONTRACT_CLIP_I64>(g, D, bias);
+    case QH_CONTRACT_DIV_RINT: return contract_ct<QH_CONTRACT_DIV_RINT>(g, D, bias);
+    case QH_CONTRACT_FLOOR256_DIV_RINT: return contract_ct<QH_CONTRACT_FLOOR256_DIV_RINT>(g, D, bias);
+    case QH_CONTRACT_ROUND_DIV: return contract_ct<QH_CONTRACT_ROUND_DIV>(g, D, bias);
+    case QH_CONTRACT_U8_DRAIN: return contract_ct<QH_CONTRACT_U8_DRAIN>(g, D, bias);
   }
   return 0;
 }
@@ -334,6 +338,296 @@ __global__ __launch_bounds__(kExThreads, 2) void qmm_exact_kernel(const ExactArg
   }
 }
 
+// ---- fused integer-contract chains: every step of a CHAIN graph in one launch
+//
+// Row m of step i+1's activation is row m of step i's output, so a workgroup that owns a block
+// of rows runs the whole chain on its own: the block's activation stays in LDS (two buffers,
+// the step's input and its output), each wave keeps its 32 weight columns in registers for all
+// steps (K == N <= 256: at most 4 x 2 x 2 fragments of 16 bytes per lane), and one barrier per
+// step separates a step's writes from the next step's reads.  16-row blocks on
+// v_mfma_i32_16x16x64_i8 give twice the workgroups of 32-row blocks (256 rows: 16 compute
+// units) and half the work per step.  Every step is the contract kernel's arithmetic (the same
+// int32 sums of the shifted operands, per-column correction and contract), so the result is the
+// per-step launches' result bit for bit; K <= 256 keeps every int32 MFMA sum below 2^22 in
+// magnitude.  The k loop always runs the 4 steps of K = 256: LDS columns K..255 hold the code
+// that shifts to 0 (0x80 bytes) and the weight fragments there are zero, so they add nothing.
+constexpr int kChRows = 16;                 // activation rows per workgroup
+constexpr int kChWaves = 8;                 // wave w owns output columns [32 w, 32 w + 32)
+constexpr int kChMaxK = 32 * kChWaves;      // K == N <= 256
+constexpr int kChSteps = kChMaxK / 64;      // 64-k MFMA steps
+constexpr int kChThreads = 64 * kChWaves;
+
+// The dividing contracts in float64 without a division, on D as an integer-valued double
+// (|D| < 2^40: every product and sum below is an exact integer).
+//  * rint(double(D) / d + zp): y = D rcp + zp (rcp = fl(1 / d), one fma) is within 2^-34 of
+//    X = D / d + zp whenever rint(y) lies in [-1, qmax + 1] (then |D / d| < 2^17 and y < 2^17).
+//    If y is also more than 2^-20 from the nearest half-integer, rint(y) = rint(X).  The
+//    float64 division rounds the same X for every output that is not clipped: a quotient that
+//    is not a tie lies at least 1 / (2 d) >= 2^-31 from a half-integer, and the division's two
+//    roundings move it by less.  Outputs outside [-1, qmax + 1] clip the same either way.  The
+//    few outputs near a half-integer (exact ties: only for even d) take the exact remainder
+//    2 (D - (c - zp) d), which picks the neighbour the exact quotient rounds to (ties to even);
+//    a wave enters that branch only when one of its lanes needs it.
+//  * floor(n / d) (round_div, n >= 0): floor(n rcp) is within one; the remainder fixes it.
+template <int CT>
+__device__ __forceinline__ int contract_chain_f64(const ExactArgs &g, double Dd, double rcp) {
+  const double dd = static_cast<double>(g.divisor), zp = static_cast<double>(g.out_zp);
+  const double qmax = static_cast<double>(g.out_qmax);
+  if constexpr (CT == QH_CONTRACT_ROUND_DIV) {
+    const double n = fabs(Dd) + static_cast<double>(g.divisor / 2);
+    double q = floor(n * rcp);
+    const double r = fma(-q, dd, n);
+    q = r < 0.0 ? q - 1.0 : (r >= dd ? q + 1.0 : q);
+    const double v = (Dd >= 0.0 ? q : -q) + zp;
+    return static_cast<int>(fmin(fmax(v, 0.0), qmax));
+  } else {
+    if (CT == QH_CONTRACT_FLOOR256_DIV_RINT) Dd = floor(Dd * 0x1p-8) * 256.0;  // floor division, exact
+    const double y = fma(Dd, rcp, zp);
+    double c = rint(y);
+    const bool near = fabs(y - c) > 0.5 - 0x1p-20 && c >= -1.0 && c <= qmax + 1.0;
+    if (__builtin_amdgcn_ballot_w64(near) != 0) {  // wave-uniform: rare
+      // exact for every lane: in range, c is within one of the rounded quotient (and lanes that
+      // are not near stay put); out of range, c +- 1 clips like c
+      const double r2 = 2.0 * fma(zp - c, dd, Dd);  // 2 (D - q d), q = c - zp
+      const double h = c * 0.5;
+      const bool odd = h != floor(h);
+      c = (r2 > dd || (r2 == dd && odd)) ? c + 1.0 : ((r2 < -dd || (r2 == -dd && odd)) ? c - 1.0 : c);
+    }
+    return static_cast<int>(fmin(fmax(c, 0.0), qmax));
+  }
+}
+
+// W16: int16 weights (two planes and the all-ones plane); else one int8 plane.  CT: the contract.
+template <bool A16, bool W16, int CT>
+__global__ __launch_bounds__(kChThreads, 1) void qmm_chain_kernel(const ExactArgs g, int chain) {
+  constexpr int D = A16 ? 2 : 1;       // activation digits
+  constexpr int NP = W16 ? 2 : 1;      // weight planes
+  constexpr int E = A16 ? 2 : 1;       // bytes per activation / output element
+  constexpr int kPitch = E * kChMaxK + 16;  // LDS row pitch: 16-byte skew per row spreads the banks
+  // the dividing contracts take the float64 path (bias_q is not part of them)
+  constexpr bool kF64 = CT == QH_CONTRACT_DIV_RINT || CT == QH_CONTRACT_FLOOR256_DIV_RINT || CT == QH_CONTRACT_ROUND_DIV;
+  __shared__ __align__(16) uint8_t buf[2][kChRows * kPitch];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int m0 = blockIdx.x * kChRows;
+  const bool active = 32 * wave < g.N;         // wave-uniform (N % 32 == 0)
+  const int kg = 16 * (lane >> 4);             // this lane's 16 k of a 64-k step
+  const int rowb = g.K * E;                    // bytes per activation row (a multiple of 32)
+  const double rcp = 1.0 / static_cast<double>(g.divisor > 0 ? g.divisor : 1);
+
+  // the block's activation rows into buffer 0 (rows past M repeat the last row; never stored);
+  // columns K..255 of both buffers: 0x80 bytes
+  for (int i = t; i < kChRows * (kChMaxK * E / 16); i += kChThreads) {
+    const int r = i / (kChMaxK * E / 16), c = i - r * (kChMaxK * E / 16);
+    const int mr = min(m0 + r, g.M - 1);
+    const uint4 pad = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+    const uint4 v = 16 * c < rowb ? *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(mr) * rowb + 16 * c) : pad;
+    *reinterpret_cast<uint4 *>(&buf[0][r * kPitch + 16 * c]) = v;
+    if (16 * c >= rowb) *reinterpret_cast<uint4 *>(&buf[1][r * kPitch + 16 * c]) = pad;
+  }
+  // B fragments: lane holds 16 k (kg..kg+15 of each 64-k step) of column 32 w + 16 ct + lane % 16
+  uint4 w[kChSteps][2][NP];
+  long long corr[2] = {0, 0}, bq[2] = {0, 0};
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const int n = 32 * wave + 16 * ct + (lane & 15);
+#pragma unroll
+    for (int s = 0; s < kChSteps; ++s)
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        w[s][ct][p] = active && 64 * s + kg < g.K ? load_w16(g, plane_col(p, n, g.layout_planes), 64 * s + kg)
+                                                  : make_uint4(0u, 0u, 0u, 0u);
+    if (active) {
+      corr[ct] = g.corr[n];
+      bq[ct] = g.bias_q ? g.bias_q[n] : 0;
+    }
+  }
+  // quad transpose of the epilogue: lane c = lane % 4 of a quad collects row c of the quad's
+  // 4 columns; round t takes the value of quad lane (c + t) % 4 (DPP quad_perm)
+  const int qc = lane & 3;
+  uint32_t qsel[4];
+#pragma unroll
+  for (int tt = 1; tt < 4; ++tt) {
+    const int k = (qc + tt) & 3;  // byte k of the result <- byte qc of the value from quad lane k
+    uint32_t sel = 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) sel |= static_cast<uint32_t>(m == k ? 4 + qc : m) << (8 * m);
+    qsel[tt] = sel;
+  }
+  __syncthreads();
+
+  for (int it = 0; it < chain; ++it) {
+    const uint8_t *src = buf[it & 1];
+    uint8_t *dst = buf[(it + 1) & 1];
+    if (active) {
+      v4i acc[2][NP][D];
+      int rs = 0;  // W16: partial sum of this lane's activation row (lane % 16) over its k
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+          for (int d = 0; d < D; ++d) acc[ct][p][d] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < kChSteps; ++s) {
+        const uint8_t *ap = src + (lane & 15) * kPitch + E * (64 * s + kg);
+        v4i af[D];
+        if (!A16) {
+          const uint4 v = *reinterpret_cast<const uint4 *>(ap);
+          af[0] = v4i{static_cast<int>(v.x ^ 0x80808080u), static_cast<int>(v.y ^ 0x80808080u),
+                      static_cast<int>(v.z ^ 0x80808080u), static_cast<int>(v.w ^ 0x80808080u)};
+        } else {
+          uint4 v0 = reinterpret_cast<const uint4 *>(ap)[0], v1 = reinterpret_cast<const uint4 *>(ap)[1];
+          v0.x ^= 0x80808080u; v0.y ^= 0x80808080u; v0.z ^= 0x80808080u; v0.w ^= 0x80808080u;
+          v1.x ^= 0x80808080u; v1.y ^= 0x80808080u; v1.z ^= 0x80808080u; v1.w ^= 0x80808080u;
+          // a - 32768 = 256 hi + lo' + 128 with hi = high byte ^ 0x80, lo' = low byte ^ 0x80
+          af[0] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x07050301u)), static_cast<int>(perm(v0.w, v0.z, 0x07050301u)),
+                      static_cast<int>(perm(v1.y, v1.x, 0x07050301u)), static_cast<int>(perm(v1.w, v1.z, 0x07050301u))};
+          af[D - 1] = v4i{static_cast<int>(perm(v0.y, v0.x, 0x06040200u)), static_cast<int>(perm(v0.w, v0.z, 0x06040200u)),
+                          static_cast<int>(perm(v1.y, v1.x, 0x06040200u)), static_cast<int>(perm(v1.w, v1.z, 0x06040200u))};
+        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const uint4 b = w[s][ct][p];
+            const v4i bv = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+              acc[ct][p][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[d], bv, acc[ct][p][d], 0, 0, 0);
+          }
+        if (W16) {
+          // the all-ones plane's product is the row sum of the shifted activation (byte dot
+          // products instead of an MFMA)
+          int part[D];
+#pragma unroll
+          for (int d = 0; d < D; ++d)
+            part[d] = __builtin_amdgcn_sdot4(af[d][0], 0x01010101, __builtin_amdgcn_sdot4(af[d][1], 0x01010101,
+                      __builtin_amdgcn_sdot4(af[d][2], 0x01010101, __builtin_amdgcn_sdot4(af[d][3], 0x01010101, 0, false),
+                                             false), false), false);
+          rs += A16 ? 256 * part[0] + part[D - 1] : part[0];
+        }
+      }
+      int rowsum = 0;
+      if (W16) {  // lane r < 16: row r over all k (its 4 k-groups sit in lanes r, r + 16, r + 32, r + 48)
+        rowsum = rs + __shfl_xor(rs, 16, 64);
+        rowsum += __shfl_xor(rowsum, 32, 64);
+      }
+      // lane holds rows 4 (lane / 16) + i, i < 4, of column 32 w + 16 ct + lane % 16
+      const int rbase = 4 * (lane >> 4);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        int v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (kF64) {
+            // D as an exact integer-valued double (|D| < 2^40)
+            double Dd;
+            if constexpr (!A16 && !W16) {
+              Dd = static_cast<double>(acc[ct][0][0][i] + static_cast<int>(corr[ct]));
+            } else if constexpr (!W16) {
+              // one plane with multiplier 1: 256 hi + lo stays below 2^31 in magnitude
+              Dd = static_cast<double>(256 * acc[ct][0][0][i] + acc[ct][0][D - 1][i]) + static_cast<double>(corr[ct]);
+            } else {
+              Dd = static_cast<double>(corr[ct]);
+#pragma unroll
+              for (int p = 0; p < NP; ++p) {
+                const double x = A16 ? fma(256.0, static_cast<double>(acc[ct][p][0][i]), static_cast<double>(acc[ct][p][D - 1][i]))
+                                     : static_cast<double>(acc[ct][p][0][i]);
+                Dd = fma(x, static_cast<double>(g.cm[p]), Dd);
+              }
+              if (W16) Dd = fma(static_cast<double>(__shfl(rowsum, rbase + i, 64)), static_cast<double>(g.ones), Dd);
+            }
+            v[i] = contract_chain_f64<CT>(g, Dd, rcp);
+          } else {
+            long long Dv;
+            if constexpr (!A16 && !W16) {
+              // one int8 plane with multiplier 1: |sum| < 2^22 and |corr| < 2^22, so int32 is exact
+              Dv = static_cast<long long>(acc[ct][0][0][i] + static_cast<int>(corr[ct]));
+            } else {
+              Dv = corr[ct];
+#pragma unroll
+              for (int p = 0; p < NP; ++p) {
+                const long long x = A16 ? 256LL * acc[ct][p][0][i] + acc[ct][p][D - 1][i] : static_cast<long long>(acc[ct][p][0][i]);
+                Dv += x * g.cm[p];
+              }
+              if (W16) Dv += static_cast<long long>(__shfl(rowsum, rbase + i, 64)) * g.ones;
+            }
+            v[i] = contract_ct<CT>(g, Dv, bq[ct]);
+          }
+        }
+        const int col0 = 32 * wave + 16 * ct + (lane & 12);  // the quad's first column
+        if (!A16) {
+          // rows rbase .. rbase + 3 of this column as bytes, then the quad transpose: lane qc
+          // ends with row rbase + qc of columns col0 .. col0 + 3
+          const uint32_t P = static_cast<uint32_t>(v[0]) | (static_cast<uint32_t>(v[1]) << 8) |
+                             (static_cast<uint32_t>(v[2]) << 16) | (static_cast<uint32_t>(v[3]) << 24);
+          uint32_t Q = P;  // round 0: byte qc of its own value is already in place
+          Q = perm(static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(P), 0x39, 0xf, 0xf, false)), Q, qsel[1]);
+          Q = perm(static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(P), 0x4E, 0xf, 0xf, false)), Q, qsel[2]);
+          Q = perm(static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(P), 0x93, 0xf, 0xf, false)), Q, qsel[3]);
+          *reinterpret_cast<uint32_t *>(dst + (rbase + qc) * kPitch + col0) = Q;
+        } else {
+          // pairs of lanes (columns c, c + 1) swap halves: the even lane ends with rows rbase and
+          // rbase + 2 of both columns, the odd lane with rows rbase + 1 and rbase + 3
+          const bool odd = lane & 1;
+          const uint32_t send = odd ? (static_cast<uint32_t>(v[0]) | (static_cast<uint32_t>(v[2]) << 16))
+                                    : (static_cast<uint32_t>(v[1]) | (static_cast<uint32_t>(v[3]) << 16));
+          const uint32_t got = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(send), 0xB1, 0xf, 0xf, false));
+          const int c2 = 32 * wave + 16 * ct + (lane & 14);  // the pair's even column
+          const uint32_t lo = odd ? (got & 0xFFFFu) | (static_cast<uint32_t>(v[1]) << 16)
+                                  : static_cast<uint32_t>(v[0]) | (got << 16);
+          const uint32_t hi = odd ? (got >> 16) | (static_cast<uint32_t>(v[3]) << 16)
+                                  : static_cast<uint32_t>(v[2]) | (got & 0xFFFF0000u);
+          const int r0 = rbase + (odd ? 1 : 0);
+          *reinterpret_cast<uint32_t *>(dst + r0 * kPitch + 2 * c2) = lo;
+          *reinterpret_cast<uint32_t *>(dst + (r0 + 2) * kPitch + 2 * c2) = hi;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // the last step's rows (those below M) to the output, 16 bytes per store
+  const uint8_t *res = buf[chain & 1];
+  const int outb = g.N * E;
+  for (int i = t; i < kChRows * (outb / 16); i += kChThreads) {
+    const int r = i / (outb / 16), c = i - r * (outb / 16);
+    if (m0 + r < g.M)
+      *reinterpret_cast<uint4 *>(static_cast<uint8_t *>(g.out) + static_cast<size_t>(m0 + r) * outb + 16 * c) =
+          *reinterpret_cast<const uint4 *>(&res[r * kPitch + 16 * c]);
+  }
+}
+
+template <bool A16, bool W16>
+qh_status launch_chain_ct(const ExactArgs &g, int chain, dim3 grid, hipStream_t stream) {
+  switch (g.contract) {
+    case QH_CONTRACT_CLIP_I32:
+      hipLaunchKernelGGL((qmm_chain_kernel<A16, W16, QH_CONTRACT_CLIP_I32>), grid, dim3(kChThreads), 0, stream, g, chain);
+      break;
+    case QH_CONTRACT_CLIP_I64:
+      hipLaunchKernelGGL((qmm_chain_kernel<A16, W16, QH_CONTRACT_CLIP_I64>), grid, dim3(kChThreads), 0, stream, g, chain);
+      break;
+    case QH_CONTRACT_DIV_RINT:
+      hipLaunchKernelGGL((qmm_chain_kernel<A16, W16, QH_CONTRACT_DIV_RINT>), grid, dim3(kChThreads), 0, stream, g, chain);
+      break;
+    case QH_CONTRACT_FLOOR256_DIV_RINT:
+      hipLaunchKernelGGL((qmm_chain_kernel<A16, W16, QH_CONTRACT_FLOOR256_DIV_RINT>), grid, dim3(kChThreads), 0, stream, g,
+                         chain);
+      break;
+    case QH_CONTRACT_ROUND_DIV:
+      hipLaunchKernelGGL((qmm_chain_kernel<A16, W16, QH_CONTRACT_ROUND_DIV>), grid, dim3(kChThreads), 0, stream, g, chain);
+      break;
+    case QH_CONTRACT_U8_DRAIN:
+      hipLaunchKernelGGL((qmm_chain_kernel<A16, W16, QH_CONTRACT_U8_DRAIN>), grid, dim3(kChThreads), 0, stream, g, chain);
+      break;
+    default:
+      return fail(QH_STATUS_UNSUPPORTED, "fused chain: unknown contract %d", g.contract);
+  }
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "qmm_chain_kernel launch");
+  return QH_STATUS_OK;
+}
+
 template <bool A16, int MODE>
 qh_status launch(const ExactArgs &g, hipStream_t stream) {
   const dim3 grid((g.N + kExTile - 1) / kExTile, (g.M + kExTile - 1) / kExTile);
@@ -350,11 +644,11 @@ qh_status dispatch(const ExactArgs &g, bool a16, hipStream_t stream) {
 
 }  // namespace
 
-qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, void *out, int mode, int contract,
-                           int divisor, hipStream_t stream) {
+namespace {
+
+ExactArgs exact_args(const qh_qmm_prepared *p, int m, const void *act, void *out, int mode, int contract, int divisor) {
   const QmmShape &sh = p->shape;
   const QmmDevice &Dv = p->dev;
-  if (m > 65535 * kExTile) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "M=%d too large for one launch", m);
   ExactArgs g{};
   g.act = static_cast<const uint8_t *>(act);
   g.out = out;
@@ -398,10 +692,36 @@ qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, voi
     g.gshift = 6;
     g.corr = Dv.corr_int;
   }
-  const bool a16 = sh.act_bits == 16;
+  return g;
+}
+
+}  // namespace
+
+qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, void *out, int mode, int contract,
+                           int divisor, hipStream_t stream) {
+  if (m > 65535 * kExTile) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "M=%d too large for one launch", m);
+  const ExactArgs g = exact_args(p, m, act, out, mode, contract, divisor);
+  const bool a16 = p->shape.act_bits == 16;
   if (mode == 0) return dispatch<0>(g, a16, stream);
   if (mode == 1) return dispatch<1>(g, a16, stream);
   return dispatch<2>(g, a16, stream);
+}
+
+bool chain_fusable(const qh_qmm_prepared *p) {
+  const QmmShape &sh = p->shape;
+  // one int8 plane with multiplier 1, or the int16 weight's two planes plus the all-ones plane
+  const bool planes = sh.int_planes == 1 ? sh.int_mult[0] == 1 && sh.int_ones == 0 : sh.int_planes == 2 && sh.int_ones != 0;
+  return planes && sh.K == sh.N && sh.K <= kChMaxK && sh.K % 32 == 0 && sh.act_bits == sh.out_bits;
+}
+
+qh_status launch_qmm_chain(const qh_qmm_prepared *p, int m, int chain, const void *act, void *out, int contract,
+                           int divisor, hipStream_t stream) {
+  if (!chain_fusable(p)) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "fused chain: K == N <= %d only", kChMaxK);
+  const ExactArgs g = exact_args(p, m, act, out, 2, contract, divisor);
+  const dim3 grid((m + kChRows - 1) / kChRows);
+  const bool a16 = p->shape.act_bits == 16, w16 = g.nplanes == 2;
+  if (a16) return w16 ? launch_chain_ct<true, true>(g, chain, grid, stream) : launch_chain_ct<true, false>(g, chain, grid, stream);
+  return w16 ? launch_chain_ct<false, true>(g, chain, grid, stream) : launch_chain_ct<false, false>(g, chain, grid, stream);
 }
 
 }  // namespace qh

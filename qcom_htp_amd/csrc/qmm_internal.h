@@ -186,6 +186,10 @@ qh_status launch_qmm_accumulate(const qh_qmm_prepared *p, int m, const void *act
 // mode 0: requantised output (per-group weights), 1: int64 accumulators, 2: integer contract
 qh_status launch_qmm_exact(const qh_qmm_prepared *p, int m, const void *act, void *out, int mode, int contract,
                            int divisor, hipStream_t stream);
+// Every step of an integer-contract chain in one launch, for K == N <= 256 (chain_fusable).
+bool chain_fusable(const qh_qmm_prepared *p);
+qh_status launch_qmm_chain(const qh_qmm_prepared *p, int m, int chain, const void *act, void *out, int contract,
+                           int divisor, hipStream_t stream);
 qh_status launch_gdn_solve_f32(const float *A, float *T, int heads, int C, int precision, hipStream_t stream);
 qh_status launch_gdn_solve_u16(const uint16_t *A, uint16_t *T, int heads, int C, int zpA, int zpT, float sA,
                                float sT, int precision, hipStream_t stream);

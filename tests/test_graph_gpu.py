@@ -223,3 +223,110 @@ def test_w4a16_precision_suite(gpu, case):
             assert np.array_equal(got, want), f"chain {chain}: {diff_msg(got, want)}"
     finally:
         op.close()
+
+
+# ------------------------------------------------------- fused integer-contract chains (one launch)
+
+
+def _mid_divisors(acc, out_bits):
+    """Divisors that keep a contract's outputs spread over the output range, so that later steps
+    of a chain see unsaturated activations: (name, divisor) for every contract."""
+    qmax = (1 << out_bits) - 1
+    d = max(1, int(round(float(np.std(acc)) / ((qmax + 1) / 6.0))))
+    half = int(np.array([512.0 / d], np.float16).view(np.uint16)[0])
+    out = [("clip_i32", 1), ("clip_i64", 1), ("div_rint", d), ("div_rint", 127), ("floor256_div_rint", d),
+           ("round_div", d), ("round_div", 7)]
+    if out_bits == 8:
+        out.append(("u8_drain", half | ((128 << 7) << 16)))  # baseline 16384: + 128
+    return out
+
+
+@pytest.mark.parametrize("fam", ["u8i8", "w4a8_per_channel", "w4a8_lpbq", "w8a16", "w4a16_lpbq", "w4a8_per_group",
+                                 "w4a16_per_group"])
+@pytest.mark.parametrize("mk", [(1, 64), (45, 192), (256, 256), (33, 320)], ids=lambda s: f"m{s[0]}_k{s[1]}")
+def test_contract_chain_matches_oracle_and_single_steps(gpu, fam, mk):
+    """An integer-contract chain with K == N <= 256 runs every step in one launch (intermediate
+    activations on chip); K = N = 320 takes one launch per step.  Either way, 5 steps equal the
+    oracle's contract applied 5 times and 5 single-step contract launches, for every contract."""
+    import torch
+
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    m, k = mk
+    c = C.synthetic_case(fam, m, k, k, seed=m + k)
+    F = c.family
+    op = QuantMatmul.from_case(c, device=gpu)
+    act = torch.from_numpy(c.activation_q).to(gpu)
+    acc1 = oq.int_accumulator(c.activation_q, c.weight_int_nk, F.act_zp)
+    try:
+        for name, d in _mid_divisors(acc1, F.out_bits):
+            print(f"[graph] fused chain {fam} m={m} k=n={k} {name}/{d}", flush=True)
+            want = oracle_chain(c, 5, name, d)
+            got = op.chain(act, 5, name, d).cpu().numpy()
+            assert np.array_equal(got, want), f"{name}/{d}: {diff_msg(got, want)}"
+            cur = act
+            for _ in range(5):
+                cur = op.run_contract(cur, name, d)
+            assert np.array_equal(cur.cpu().numpy(), want), f"single steps {name}/{d}"
+    finally:
+        op.close()
+
+
+@pytest.mark.parametrize("mk", [(1, 32), (70, 256), (256, 256)], ids=lambda s: f"m{s[0]}_k{s[1]}")
+def test_w16a16_contract_chain_matches_oracle(gpu, mk):
+    """int16 weights (two byte planes and the all-ones plane) through the one-launch chain:
+    5 steps of the W16A16 requantisation contract against the oracle's int16 accumulator."""
+    import torch
+
+    from qcom_htp_amd import _lib
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    m, k = mk
+    rng = np.random.default_rng(m * 7 + k)
+    x = rng.integers(0, 65536, size=(m, k)).astype(np.uint16)
+    q16 = rng.integers(-32768, 32768, size=(k, k)).astype(np.int16)
+    q16[:, 0] = 32767
+    q16[:, 1] = -32768
+    op = QuantMatmul(q16, None, None, act_bits=16, out_bits=16, act_scale=1.0, out_scale=1.0, act_zp=32768,
+                     out_zp=32768, weight_format=_lib.QH_WEIGHT_I16, device=gpu)
+    try:
+        acc1 = oq.w16a16_accumulator(x, q16, 32768)
+        d = max(1, int(round(float(np.std(acc1)) / (65536 / 6.0))))
+        for name, dd in (("div_rint", 32767), ("div_rint", d), ("round_div", d)):
+            print(f"[graph] fused w16a16 chain m={m} k=n={k} {name}/{dd}", flush=True)
+            cur = x
+            for _ in range(5):
+                cur = oq.contract_output(oq.w16a16_accumulator(cur, q16, 32768), name, dd, None, 32768, 16)
+            got = op.chain(torch.from_numpy(x).to(gpu), 5, name, dd).cpu().numpy()
+            assert np.array_equal(got, cur), f"{name}/{dd}: {diff_msg(got, cur)}"
+    finally:
+        op.close()
+
+
+def test_contract_chain_graph_replays(gpu):
+    """The one-launch contract chain captured in a HIP graph: every replay equals the eager chain
+    (the kernel allocates nothing and clears nothing with memset)."""
+    import torch
+
+    from qcom_htp_amd.qmm import QuantMatmul
+
+    c = C.synthetic_case("w4a8_lpbq", 256, 256, 256, seed=5)
+    op = QuantMatmul.from_case(c, device=gpu)
+    try:
+        act = torch.from_numpy(c.activation_q).to(gpu)
+        eager = op.chain(act, 8, "div_rint", 300).clone()
+        out = torch.empty_like(eager)
+        scratch = torch.empty_like(eager)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            op.chain(act, 8, "div_rint", 300, out=out, scratch=scratch)
+        for rep in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {rep}"
+        np.testing.assert_array_equal(eager.cpu().numpy(), oracle_chain(c, 8, "div_rint", 300))
+    finally:
+        op.close()
