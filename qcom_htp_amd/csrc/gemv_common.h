@@ -15,6 +15,7 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 }
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // int8 weight bytes of 4 int4 codes: nibbles u (offset-binary, code = u - 8) times the LPBQ block
@@ -75,6 +76,22 @@ __device__ __forceinline__ uint4 load_stream(const uint8_t *p) {
   const v4u x = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
   return make_uint4(x.x, x.y, x.z, x.w);
 }
+
+// Buffer loads: an offset at or past `bytes` returns zero without a memory access (and a
+// resource of 0 bytes turns every load of it into such a load, still counted like the others).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+template <int AUX = 0>
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
+constexpr int kNT = 2;  // buffer-load cache policy: nontemporal (the weights are read once per call)
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);

@@ -75,29 +75,43 @@ __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, 
   // a - zp = plane value + off (8-bit: a - 128; 16-bit: 256 hi + lo' with a - 32768 - 128)
   const int off = (A16 ? 32768 + 128 : 128) - g.act_zp;
   double s = 0.0;
-  for (int kg = lane; kg < KG; kg += 64) {
-    uint32_t wd[WB / 4];
-    const uint4 *p = reinterpret_cast<const uint4 *>(wcol + static_cast<size_t>(kg) * 16 * WB);
+  // a lane's k-groups (up to kPre of them: all of them for K <= 8192) are requested before any
+  // is used, so the pass costs one memory round trip
+  constexpr int kPre = 4;
+  for (int kg0 = lane; kg0 < KG; kg0 += 64 * kPre) {
+    uint32_t wd[kPre][WB / 4];
+    int fs[kPre];
 #pragma unroll
-    for (int q = 0; q < WB / 16; ++q) {
-      const uint4 v = p[q];
-      wd[4 * q] = v.x; wd[4 * q + 1] = v.y; wd[4 * q + 2] = v.z; wd[4 * q + 3] = v.w;
-    }
-    const int f = LPBQ ? g.lpbq[gemv_scale_index_kg(n, kg, g.nbatch, g.sub_shift)] : 1;
-    const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
-    const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * g.ars + kg * 32);
-#pragma unroll 4
-    for (int j = 0; j < 32; ++j) {
-      int w;
-      if (FMT == kTileI4) {
-        const uint32_t byte = (wd[(j & 15) >> 2] >> (8 * (j & 3))) & 0xFFu;
-        w = ((j < 16 ? (byte & 15u) : (byte >> 4)) - 8) * f;
-      } else {
-        w = static_cast<int8_t>((wd[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+    for (int u = 0; u < kPre; ++u) {
+      const int kg = min(kg0 + 64 * u, KG - 1);
+      const uint4 *p = reinterpret_cast<const uint4 *>(wcol + static_cast<size_t>(kg) * 16 * WB);
+#pragma unroll
+      for (int q = 0; q < WB / 16; ++q) {
+        const uint4 v = p[q];
+        wd[u][4 * q] = v.x; wd[u][4 * q + 1] = v.y; wd[u][4 * q + 2] = v.z; wd[u][4 * q + 3] = v.w;
       }
-      const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : static_cast<int>(hp[j])) + off;
-      const float wf = static_cast<float>(w) * sc;
-      s = fma(static_cast<double>(a) * g.sA, static_cast<double>(wf), s);
+      fs[u] = LPBQ ? g.lpbq[gemv_scale_index_kg(n, kg, g.nbatch, g.sub_shift)] : 1;
+    }
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int kg = kg0 + 64 * u;
+      if (kg >= KG) break;
+      const int f = fs[u];
+      const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
+      const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * g.ars + kg * 32);
+#pragma unroll 4
+      for (int j = 0; j < 32; ++j) {
+        int w;
+        if (FMT == kTileI4) {
+          const uint32_t byte = (wd[u][(j & 15) >> 2] >> (8 * (j & 3))) & 0xFFu;
+          w = ((j < 16 ? (byte & 15u) : (byte >> 4)) - 8) * f;
+        } else {
+          w = static_cast<int8_t>((wd[u][j >> 2] >> (8 * (j & 3))) & 0xFFu);
+        }
+        const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : static_cast<int>(hp[j])) + off;
+        const float wf = static_cast<float>(w) * sc;
+        s = fma(static_cast<double>(a) * g.sA, static_cast<double>(wf), s);
+      }
     }
   }
 #pragma unroll
@@ -278,23 +292,32 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   const int iters = (KG + 15) / 16;  // k-group slots per lane (some past KG when KG % 16 != 0)
   // One batch of kU k-groups per lane: the weight words and their LPBQ block scales (one
   // 8-byte load of the lane's kU scales).
-  uint4 wv[kU][FMT == kTileI4 ? 1 : 2];
+  constexpr int WV = FMT == kTileI4 ? 1 : 2;
+  uint4 wv[kU][WV];
   uint2 fsv = make_uint2(0x01010101u, 0x01010101u);
+  constexpr bool kLoop = MM == 16;  // 16 rows: workgroups loop over groups
   // Straight-line loads (indices clamped, results of slots past KG discarded) keep every load
   // of a batch in one basic block, so they issue back to back and their waits count down.
-  auto issue = [&](int grp, int i0) {
-    const uint8_t *const wgrp = g.w + static_cast<size_t>(grp) * KG * 16 * WB;
+  // Buffer loads; a group that does not exist (grp >= groups) gets a resource of 0 bytes, so
+  // its loads return zeros without touching memory and every load count stays the same.
+  const uint32_t wbytes = static_cast<uint32_t>(KG) * 16 * WB;
+  const uint32_t lbytes = LPBQ ? static_cast<uint32_t>(gemv_scale_index(groups, 0, g.nbatch, 0, 0, 4 >> g.sub_shift, 0, 0)) : 0u;
+  auto issue_into = [&](int grp, int i0, auto &dst, uint2 &fdst) {
+    const bool real = grp < groups;
+    const int gi = real ? grp : 0;
+    const auto rw = rsrc(g.w + static_cast<size_t>(gi) * wbytes, real ? wbytes : 0u);
     if (LPBQ)  // first: slot 0 needs it, and loads complete in order
-      fsv = *reinterpret_cast<const uint2 *>(g.lpbq + gemv_scale_index(grp, i0 / kU, g.nbatch, wave, sub >> g.sub_shift,
-                                                                       4 >> g.sub_shift, col, 0));
+      fdst = bload8(rsrc(g.lpbq, real ? lbytes : 0u),
+                    static_cast<uint32_t>(gemv_scale_index(gi, i0 / kU, g.nbatch, wave, sub >> g.sub_shift, 4 >> g.sub_shift, col, 0)));
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
       const int kg = min(4 * (wave + 4 * (i0 + i)) + sub, KG - 1);
-      const uint8_t *p = wgrp + (static_cast<size_t>(kg) * 16 + col) * WB;
-      wv[i][0] = load_stream(p);
-      if (FMT != kTileI4) wv[i][FMT == kTileI4 ? 0 : 1] = load_stream(p + 16);
+      const uint32_t off = (static_cast<uint32_t>(kg) * 16 + col) * WB;
+      dst[i][0] = bload16<kNT>(rw, off);
+      if (FMT != kTileI4) dst[i][WV - 1] = bload16<kNT>(rw, off + 16);
     }
   };
+  auto issue = [&](int grp, int i0) { issue_into(grp, i0, wv, fsv); };
   // Per-output epilogue constants of thread t's output (row t / 16, column t % 16 of the
   // group), requested together with the group's first batch of weights.
   struct Epi {
@@ -302,37 +325,71 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     int64_t corr, mant, csr;
   } ep{};
   const bool owns_out = t < MM * 16 && (t >> 4) < M;
-  auto load_epi = [&](int grp) {  // every thread loads (its column exists), only owners use it
+  auto epi_of = [&](int grp) {  // every thread loads (its column exists), only owners use it
+    Epi e{};
     const int n = grp * 16 + (t & 15);
-    ep.alpha = g.alpha[n];
-    ep.beta = g.beta[n];
-    ep.margin = g.margin[n];
-    ep.absb = g.absb[n];
+    e.alpha = g.alpha[n];
+    e.beta = g.beta[n];
+    e.margin = g.margin[n];
+    e.absb = g.absb[n];
     if (A16) {
-      ep.corr = g.colsum[n];
-      ep.mr1 = HR ? g.mlo[n] : g.mr1[n];
-      ep.mant = g.mant[n];
-      if (HR) ep.csr = g.colsum_r[n];
+      e.corr = g.colsum[n];
+      e.mr1 = HR ? g.mlo[n] : g.mr1[n];
+      e.mant = g.mant[n];
+      if (HR) e.csr = g.colsum_r[n];
     } else {
-      ep.corr = g.corr[n];
+      e.corr = g.corr[n];
+    }
+    return e;
+  };
+  auto load_epi = [&](int grp) { ep = epi_of(grp); };
+  // Residue tables of a group's 16 columns (HR): the column mantissas of the table entries this
+  // thread fills, (column, f) = (e / kRtabF, e % kRtabF) for e = t and t + 256
+  constexpr int kRtabE = (16 * kRtabF + kGemvThreads - 1) / kGemvThreads;
+  auto rtab_mant = [&](int grp, int (&mt)[kRtabE]) {
+#pragma unroll
+    for (int j = 0; j < kRtabE; ++j) {
+      const int e = min(t + j * kGemvThreads, 16 * kRtabF - 1);
+      mt[j] = static_cast<int>(g.mant[grp * 16 + e / kRtabF]);
     }
   };
+  int rmt[HR ? kRtabE : 1] = {};
   // The first activation unit and the first batch of weights are requested before anything
   // waits: the staging then overlaps the weight stream.
   ActUnit<A16> au;
   const int units = M * KG;
-  load_unit<A16>(g, min(t, units - 1), au);
-  issue(blockIdx.x, 0);  // the launch never has more workgroups than groups
-  load_epi(blockIdx.x);
-  if (t < 16) r1[t] = 0;
-  if (t == 0) fix_cnt = 0;
-  lds_barrier();
-  if (t < units) store_unit<A16, FMT>(g, t, au, lds, r1);
   // further units: for 16 rows a batch of loads is issued before its first LDS store (a
   // load-then-store loop would wait for every load in turn); fewer rows have one or two units
   // per thread and no registers to spare under their occupancy bound
   constexpr int kStageB = MM < 16 ? 1 : (A16 ? 4 : 8);
-  for (int u0 = t + kGemvThreads; u0 < units; u0 += kGemvThreads * kStageB) {
+  int ustart = t + kGemvThreads;  // the first unit of the staging loop below
+  if constexpr (kLoop) {
+    // 16 rows: the staged activations (L2) are requested first, then the per-group constants
+    // and the first group's weights (HBM): one counter tracks the loads in order, so the staging
+    // waits for its own loads only and overlaps the weights' latency.
+    ActUnit<A16> s0[kStageB];
+#pragma unroll
+    for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(t + j * kGemvThreads, units - 1), s0[j]);
+    if constexpr (HR) rtab_mant(blockIdx.x, rmt);
+    load_epi(blockIdx.x);
+    issue(blockIdx.x, 0);
+    if (t < 16) r1[t] = 0;
+    if (t == 0) fix_cnt = 0;
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < kStageB; ++j)
+      if (t + j * kGemvThreads < units) store_unit<A16, FMT>(g, t + j * kGemvThreads, s0[j], lds, r1);
+    ustart = t + kStageB * kGemvThreads;
+  } else {
+    load_unit<A16>(g, min(t, units - 1), au);
+    issue(blockIdx.x, 0);  // the launch never has more workgroups than groups
+    load_epi(blockIdx.x);
+    if (t < 16) r1[t] = 0;
+    if (t == 0) fix_cnt = 0;
+    lds_barrier();
+    if (t < units) store_unit<A16, FMT>(g, t, au, lds, r1);
+  }
+  for (int u0 = ustart; u0 < units; u0 += kGemvThreads * kStageB) {
     ActUnit<A16> ub[kStageB];
 #pragma unroll
     for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(u0 + j * kGemvThreads, units - 1), ub[j]);
@@ -344,15 +401,21 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
 
   // Workgroups loop over groups only for 16 rows (whose staging is amortised over several
   // groups); otherwise each workgroup owns exactly one group.
-  constexpr bool kLoop = MM == 16;
   // 16 rows: the k-group products run on the matrix core (the dot4 path reads every activation
   // row from LDS once per weight word and is LDS bound there)
   constexpr bool kMfma = MM == 16;
   for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
     if constexpr (HR) {
       // residue tables of this group's 16 columns, one (column, f) per thread and step
-      for (int e = t; e < 16 * kRtabF; e += kGemvThreads)
-        rtab[e] = resid_table(static_cast<int>(g.mant[grp * 16 + e / kRtabF]), e % kRtabF);
+      if constexpr (kLoop) {
+        // mantissas requested with the previous group's epilogue constants
+#pragma unroll
+        for (int j = 0; j < kRtabE; ++j)
+          if (t + j * kGemvThreads < 16 * kRtabF) rtab[t + j * kGemvThreads] = resid_table(rmt[j], (t + j * kGemvThreads) % kRtabF);
+      } else {
+        for (int e = t; e < 16 * kRtabF; e += kGemvThreads)
+          rtab[e] = resid_table(static_cast<int>(g.mant[grp * 16 + e / kRtabF]), e % kRtabF);
+      }
       lds_barrier();
     }
     int acc[kMfma ? 1 : MM], acc2[A16 && !kMfma ? MM : 1], acc3[HR && !kMfma ? MM : 1];
@@ -478,8 +541,16 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         }
       }
     }
-    // the next group's first batch is in flight during the reduction and the epilogue
-    if (kLoop && grp + static_cast<int>(gridDim.x) < groups) issue(grp + gridDim.x, 0);
+    // 16 rows: the next group's constants, then its first batch of weights, are in flight
+    // during the reduction and the epilogue (the constants first: the next epilogue's and
+    // residue tables' waits then do not include the weights)
+    Epi ep_next{};
+    if constexpr (kLoop) {
+      const int nxt = min(grp + static_cast<int>(gridDim.x), groups - 1);
+      ep_next = epi_of(nxt);
+      if constexpr (HR) rtab_mant(nxt, rmt);
+      issue(grp + static_cast<int>(gridDim.x), 0);
+    }
     // reduce over the 4 k-group lanes of each column, then over the waves in LDS
     if constexpr (kMfma) {
       // the product already summed the wave's lanes: lane (quarter q, column c) holds rows 4 q .. + 3
@@ -589,7 +660,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     lds_barrier();  // red and the fixup list are rewritten by the next group
     if (t == 0) fix_cnt = 0;
     if (!kLoop) break;
-    if (grp + static_cast<int>(gridDim.x) < groups) load_epi(grp + gridDim.x);
+    ep = ep_next;
   }
 }
 
@@ -659,7 +730,11 @@ qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
     if (st != QH_STATUS_OK) return st;
     const int cap = resident_workgroups<A16, FMT, LPBQ>(dyn_lds);
     const int lim = cap > 0 && cap < 512 ? cap : 512;
-    if (blocks > lim) blocks = lim;
+    if (blocks > lim) {
+      // the same number of groups per workgroup (rounded up), so the workgroups end together
+      const int per = (groups + lim - 1) / lim;
+      blocks = (groups + per - 1) / per;
+    }
   }
   return launch_one<A16, FMT, LPBQ, 16>(g, dim3(blocks), dyn_lds, stream);
 }

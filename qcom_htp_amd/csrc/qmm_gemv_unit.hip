@@ -35,7 +35,6 @@
 namespace qh {
 namespace {
 
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 constexpr int kUT = 512;         // threads per workgroup
 constexpr int kUW = kUT / 64;    // waves
@@ -58,19 +57,6 @@ struct UnitArgs {
   int off_asum, off_sc, off_rec, off_rtab, off_red, off_fixw;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, static_cast<int>(bytes), 0x00020000);
-}
-template <int AUX = 0>
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const v2u v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-  return make_uint2(v.x, v.y);
-}
-constexpr int kNT = 2;  // buffer-load cache policy: nontemporal (the weights are read once per call)
 
 // Compile-time loop: f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>).
 template <class F, int... I>
