@@ -264,8 +264,19 @@ __device__ __forceinline__ void store_unit(const GemvArgs &g, int u, ActUnit<A16
   }
 }
 
+// 16 rows of 16-bit activations stage 128 KiB (one workgroup per compute unit) and need four
+// product sets per weight word: their workgroups take 8 waves, waves w and w + 4 splitting the
+// slots of one lane pattern, so that two waves per SIMD share the products.
+template <bool A16, int MM>
+constexpr int gemv_threads() {
+  return MM == 16 && A16 ? 2 * kGemvThreads : kGemvThreads;
+}
+
 template <bool A16, int FMT, bool LPBQ, int MM>
-__global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kernel(const GemvArgs g) {
+__global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2) : 4)) void qmm_gemv_kernel(const GemvArgs g) {
+  constexpr int NT = gemv_threads<A16, MM>();
+  constexpr bool kWide = NT > kGemvThreads;
+  constexpr int kUw = kWide ? kU / 2 : kU;  // slots of a batch per wave
   // 16-bit activations with int4 codes also form sum_k hi'_k r_k (the residue products of the
   // high activation byte) exactly, from the residue tables of the group's 16 columns
   constexpr bool HR = A16 && FMT == kTileI4;
@@ -283,7 +294,10 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   __shared__ int fix_cnt;
   __shared__ double dred[kFixBatch * kGemvWaves];
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  // the wave of the lane pattern (k-groups 4 (wave + 4 i) + sub) and, 8 waves, the half of the
+  // batch's slots this wave takes
+  const int wave = (t >> 6) & (kGemvWaves - 1), shalf = kWide ? (t >> 8) : 0;
   const int M = g.M, KG = g.KG;
   constexpr int WB = FMT == kTileI4 ? 16 : 32;  // stream bytes per (column, k-group)
   const int16_t *const asum = reinterpret_cast<const int16_t *>(lds + g.off_asum);
@@ -293,7 +307,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   // One batch of kU k-groups per lane: the weight words and their LPBQ block scales (one
   // 8-byte load of the lane's kU scales).
   constexpr int WV = FMT == kTileI4 ? 1 : 2;
-  uint4 wv[kU][WV];
+  uint4 wv[kUw][WV];
   uint2 fsv = make_uint2(0x01010101u, 0x01010101u);
   constexpr bool kLoop = MM == 16;  // 16 rows: workgroups loop over groups
   // Straight-line loads (indices clamped, results of slots past KG discarded) keep every load
@@ -310,11 +324,11 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
       fdst = bload8(rsrc(g.lpbq, real ? lbytes : 0u),
                     static_cast<uint32_t>(gemv_scale_index(gi, i0 / kU, g.nbatch, wave, sub >> g.sub_shift, 4 >> g.sub_shift, col, 0)));
 #pragma unroll
-    for (int i = 0; i < kU; ++i) {
-      const int kg = min(4 * (wave + 4 * (i0 + i)) + sub, KG - 1);
+    for (int ii = 0; ii < kUw; ++ii) {
+      const int kg = min(4 * (wave + 4 * (i0 + ii + shalf * kUw)) + sub, KG - 1);
       const uint32_t off = (static_cast<uint32_t>(kg) * 16 + col) * WB;
-      dst[i][0] = bload16<kNT>(rw, off);
-      if (FMT != kTileI4) dst[i][WV - 1] = bload16<kNT>(rw, off + 16);
+      dst[ii][0] = bload16<kNT>(rw, off);
+      if (FMT != kTileI4) dst[ii][WV - 1] = bload16<kNT>(rw, off + 16);
     }
   };
   auto issue = [&](int grp, int i0) { issue_into(grp, i0, wv, fsv); };
@@ -345,11 +359,11 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   auto load_epi = [&](int grp) { ep = epi_of(grp); };
   // Residue tables of a group's 16 columns (HR): the column mantissas of the table entries this
   // thread fills, (column, f) = (e / kRtabF, e % kRtabF) for e = t and t + 256
-  constexpr int kRtabE = (16 * kRtabF + kGemvThreads - 1) / kGemvThreads;
+  constexpr int kRtabE = (16 * kRtabF + NT - 1) / NT;
   auto rtab_mant = [&](int grp, int (&mt)[kRtabE]) {
 #pragma unroll
     for (int j = 0; j < kRtabE; ++j) {
-      const int e = min(t + j * kGemvThreads, 16 * kRtabF - 1);
+      const int e = min(t + j * NT, 16 * kRtabF - 1);
       mt[j] = static_cast<int>(g.mant[grp * 16 + e / kRtabF]);
     }
   };
@@ -362,14 +376,14 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
   // load-then-store loop would wait for every load in turn); fewer rows have one or two units
   // per thread and no registers to spare under their occupancy bound
   constexpr int kStageB = MM < 16 ? 1 : (A16 ? 4 : 8);
-  int ustart = t + kGemvThreads;  // the first unit of the staging loop below
+  int ustart = t + NT;  // the first unit of the staging loop below
   if constexpr (kLoop) {
     // 16 rows: the staged activations (L2) are requested first, then the per-group constants
     // and the first group's weights (HBM): one counter tracks the loads in order, so the staging
     // waits for its own loads only and overlaps the weights' latency.
     ActUnit<A16> s0[kStageB];
 #pragma unroll
-    for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(t + j * kGemvThreads, units - 1), s0[j]);
+    for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(t + j * NT, units - 1), s0[j]);
     if constexpr (HR) rtab_mant(blockIdx.x, rmt);
     load_epi(blockIdx.x);
     issue(blockIdx.x, 0);
@@ -378,8 +392,8 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     lds_barrier();
 #pragma unroll
     for (int j = 0; j < kStageB; ++j)
-      if (t + j * kGemvThreads < units) store_unit<A16, FMT>(g, t + j * kGemvThreads, s0[j], lds, r1);
-    ustart = t + kStageB * kGemvThreads;
+      if (t + j * NT < units) store_unit<A16, FMT>(g, t + j * NT, s0[j], lds, r1);
+    ustart = t + kStageB * NT;
   } else {
     load_unit<A16>(g, min(t, units - 1), au);
     issue(blockIdx.x, 0);  // the launch never has more workgroups than groups
@@ -389,13 +403,13 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     lds_barrier();
     if (t < units) store_unit<A16, FMT>(g, t, au, lds, r1);
   }
-  for (int u0 = ustart; u0 < units; u0 += kGemvThreads * kStageB) {
+  for (int u0 = ustart; u0 < units; u0 += NT * kStageB) {
     ActUnit<A16> ub[kStageB];
 #pragma unroll
-    for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(u0 + j * kGemvThreads, units - 1), ub[j]);
+    for (int j = 0; j < kStageB; ++j) load_unit<A16>(g, min(u0 + j * NT, units - 1), ub[j]);
 #pragma unroll
     for (int j = 0; j < kStageB; ++j)
-      if (u0 + j * kGemvThreads < units) store_unit<A16, FMT>(g, u0 + j * kGemvThreads, ub[j], lds, r1);
+      if (u0 + j * NT < units) store_unit<A16, FMT>(g, u0 + j * NT, ub[j], lds, r1);
   }
   lds_barrier();
 
@@ -411,9 +425,9 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         // mantissas requested with the previous group's epilogue constants
 #pragma unroll
         for (int j = 0; j < kRtabE; ++j)
-          if (t + j * kGemvThreads < 16 * kRtabF) rtab[t + j * kGemvThreads] = resid_table(rmt[j], (t + j * kGemvThreads) % kRtabF);
+          if (t + j * NT < 16 * kRtabF) rtab[t + j * NT] = resid_table(rmt[j], (t + j * NT) % kRtabF);
       } else {
-        for (int e = t; e < 16 * kRtabF; e += kGemvThreads)
+        for (int e = t; e < 16 * kRtabF; e += NT)
           rtab[e] = resid_table(static_cast<int>(g.mant[grp * 16 + e / kRtabF]), e % kRtabF);
       }
       lds_barrier();
@@ -435,7 +449,8 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
         // four products j cover each lane quarter's 32 k.
         const int mrow = min(lane & 15, M - 1);  // rows past M repeat row M - 1 (never stored)
 #pragma unroll
-        for (int i = 0; i < kU; ++i) {
+        for (int ii = 0; ii < kUw; ++ii) {
+          const int i = ii + shalf * kUw;  // the slot of the batch
           const int kg_raw = 4 * (wave + 4 * (i0 + i)) + sub;
           const bool valid = kg_raw < KG;
           const int kg = valid ? kg_raw : KG - 1;
@@ -443,7 +458,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
           uint32_t rr[HR ? 8 : 1];  // residues of the same 32 weights
           if (FMT == kTileI4) {
             const uint32_t f = valid ? (LPBQ ? ((i < 4 ? fsv.x : fsv.y) >> (8 * (i & 3))) & 0xFFu : 1u) : 0u;
-            const uint4 v = wv[i][0];
+            const uint4 v = wv[ii][0];
             if constexpr (HR) {
               const uint4 tab = rtab[col * kRtabF + f];
               rr[0] = resid4(v.x & 0x0F0F0F0Fu, tab); rr[1] = resid4(v.y & 0x0F0F0F0Fu, tab);
@@ -457,7 +472,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
             b[4] = w4_to_i8((v.x >> 4) & 0x0F0F0F0Fu, f); b[5] = w4_to_i8((v.y >> 4) & 0x0F0F0F0Fu, f);
             b[6] = w4_to_i8((v.z >> 4) & 0x0F0F0F0Fu, f); b[7] = w4_to_i8((v.w >> 4) & 0x0F0F0F0Fu, f);
           } else {
-            const uint4 v0 = wv[i][0], v1 = wv[i][FMT == kTileI4 ? 0 : 1];
+            const uint4 v0 = wv[ii][0], v1 = wv[ii][FMT == kTileI4 ? 0 : 1];
             const uint32_t mk = valid ? 0xFFFFFFFFu : 0u;
             b[0] = v0.x & mk; b[1] = v0.y & mk; b[2] = v0.z & mk; b[3] = v0.w & mk;
             b[4] = v1.x & mk; b[5] = v1.y & mk; b[6] = v1.z & mk; b[7] = v1.w & mk;
@@ -554,12 +569,27 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     // reduce over the 4 k-group lanes of each column, then over the waves in LDS
     if constexpr (kMfma) {
       // the product already summed the wave's lanes: lane (quarter q, column c) holds rows 4 q .. + 3
+      if (shalf == 0) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        red[wave][4 * sub + q][col] = macc[q];
-        if (A16) red2[wave][4 * sub + q][col] = macc2[q];
-        if (HR) red3[wave][4 * sub + q][col] = macc3[q];
-        if (LR) red4[wave][4 * sub + q][col] = macc4[q];
+        for (int q = 0; q < 4; ++q) {
+          red[wave][4 * sub + q][col] = macc[q];
+          if (A16) red2[wave][4 * sub + q][col] = macc2[q];
+          if (HR) red3[wave][4 * sub + q][col] = macc3[q];
+          if (LR) red4[wave][4 * sub + q][col] = macc4[q];
+        }
+      }
+      if constexpr (kWide) {
+        // the second half of the waves adds its sums into the first half's
+        lds_barrier();
+        if (shalf == 1) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            atomicAdd(&red[wave][4 * sub + q][col], macc[q]);
+            if (A16) atomicAdd(&red2[wave][4 * sub + q][col], macc2[q]);
+            if (HR) atomicAdd(&red3[wave][4 * sub + q][col], macc3[q]);
+            if (LR) atomicAdd(&red4[wave][4 * sub + q][col], macc4[q]);
+          }
+        }
       }
     }
 #pragma unroll
@@ -628,7 +658,7 @@ __global__ __launch_bounds__(kGemvThreads, MM == 16 ? 2 : 4) void qmm_gemv_kerne
     const int nfix = fix_cnt;
     if (kLoop || KG > kGemvBatchKG) {
       // the weight registers hold the next group or only the last batch: re-read the column
-      for (int e = wave; e < nfix; e += kGemvWaves) {
+      for (int e = t >> 6; e < nfix; e += NT / 64) {
         const int tt = fix_list[e];
         gemv_fixup<A16, FMT, LPBQ>(g, lds, tt >> 4, grp * 16 + (tt & 15), lane);
       }
@@ -688,7 +718,7 @@ template <bool A16, int FMT, bool LPBQ, int MM>
 qh_status launch_one(const GemvArgs &g, dim3 grid, size_t dyn_lds, hipStream_t stream) {
   const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, MM>();
   if (st != QH_STATUS_OK) return st;
-  hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MM>), grid, dim3(kGemvThreads), dyn_lds, stream, g);
+  hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MM>), grid, dim3(gemv_threads<A16, MM>()), dyn_lds, stream, g);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "qmm_gemv_kernel launch");
   return QH_STATUS_OK;
@@ -706,7 +736,7 @@ int resident_workgroups(size_t dyn_lds) {
   if ((hit & ~static_cast<uint64_t>(0xFFFF)) == key && (hit & 0xFFFF) != 0) return static_cast<int>(hit & 0xFFFF);
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(&qmm_gemv_kernel<A16, FMT, LPBQ, 16>),
-                                                   kGemvThreads, dyn_lds) != hipSuccess)
+                                                   gemv_threads<A16, 16>(), dyn_lds) != hipSuccess)
     return 0;
   const long long wg = static_cast<long long>(occ) * device_cu_count();
   if (wg <= 0 || wg > 0xFFFF) return 0;
