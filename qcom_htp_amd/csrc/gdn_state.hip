@@ -28,6 +28,8 @@
 // fp32 accumulation; products with the exact q, k take two terms); QH_GDN_BF16 uses the hi
 // parts only.  Norms, decays and the prefix sum are fp32.
 
+#include <type_traits>
+
 #include "bf16_split.h"
 #include "lane_ops.h"
 #include "qmm_internal.h"
@@ -61,16 +63,17 @@ __device__ __forceinline__ float bf16f(uint32_t h) { return __uint_as_float(h <<
 // One chunk's inputs as read from global memory, per thread: the row segment (token t / 8,
 // columns 16 (t % 8) ..) of q, k and W, this wave's U tiles (MFMA result layout) and one gc
 // value per lane (every wave reads the same 64; wave 0 uses them).
-template <bool WU_F32>
+template <bool WU_F32, int RP>
 struct ChunkIn {
-  uint4 q[2], k[2];
-  uint4 w[WU_F32 ? 4 : 2];
+  uint4 q[RP][2], k[RP][2];
+  uint4 w[RP][WU_F32 ? 4 : 2];
   float u[4][4];
   float gc;
 };
 
-// Per-lane element offsets of chunk 0 (a chunk adds 64 H D): the thread's row segment, its
-// wave's U / o tile elements (token 4 qd + e of tile i is + (16 i + e) H D) and lane's gc.
+// Per-lane element offsets of chunk 0 (a chunk adds 64 H D): the thread's first row segment
+// (token t / 8, or t / 8 + 32 r for its r-th), its wave's U / o tile elements (token 4 qd + e of
+// tile i is + (16 i + e) H D) and lane's gc.
 struct Offsets {
   uint32_t row, tile, g;
   uint32_t tok;  // H D: one token
@@ -84,24 +87,27 @@ __device__ __forceinline__ Offsets offsets(const StateArgs &a, int b, int h, int
           static_cast<uint32_t>(b) * a.T * a.H + lane * a.H + h, tok};
 }
 
-template <bool WU_F32>
-__device__ __forceinline__ void load_chunk(const StateArgs &a, const Offsets &of, int n, ChunkIn<WU_F32> &in) {
+template <bool WU_F32, int RP>
+__device__ __forceinline__ void load_chunk(const StateArgs &a, const Offsets &of, int n, ChunkIn<WU_F32, RP> &in) {
   const uint32_t c0 = static_cast<uint32_t>(n) * kC * of.tok;
-  const uint32_t ri = of.row + c0;
-  const uint4 *qp = reinterpret_cast<const uint4 *>(a.q + ri);
-  const uint4 *kp = reinterpret_cast<const uint4 *>(a.k + ri);
-  in.q[0] = qp[0];
-  in.q[1] = qp[1];
-  in.k[0] = kp[0];
-  in.k[1] = kp[1];
-  if constexpr (WU_F32) {
-    const uint4 *wp = reinterpret_cast<const uint4 *>(static_cast<const float *>(a.w) + ri);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) in.w[x] = wp[x];
-  } else {
-    const uint4 *wp = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.w) + ri);
-    in.w[0] = wp[0];
-    in.w[1] = wp[1];
+  for (int r = 0; r < RP; ++r) {
+    const uint32_t ri = of.row + c0 + static_cast<uint32_t>(32 * r) * of.tok;
+    const uint4 *qp = reinterpret_cast<const uint4 *>(a.q + ri);
+    const uint4 *kp = reinterpret_cast<const uint4 *>(a.k + ri);
+    in.q[r][0] = qp[0];
+    in.q[r][1] = qp[1];
+    in.k[r][0] = kp[0];
+    in.k[r][1] = kp[1];
+    if constexpr (WU_F32) {
+      const uint4 *wp = reinterpret_cast<const uint4 *>(static_cast<const float *>(a.w) + ri);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) in.w[r][x] = wp[x];
+    } else {
+      const uint4 *wp = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.w) + ri);
+      in.w[r][0] = wp[0];
+      in.w[r][1] = wp[1];
+    }
   }
   const uint32_t ti = of.tile + c0;
 #pragma unroll
@@ -149,12 +155,16 @@ __device__ __forceinline__ Half4 bf16x4_tr(const uint16_t *p) {
 }
 template <bool SPLIT, bool WU_F32, bool OUT_F32>
 __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
-  // q, k rows as given (bf16, exact MFMA operands) with their l2norm factors; W as hi | lo words;
-  // P as hi | lo words (lower tiles); g, e^g, e^{g_last - g} per token
+  constexpr int RP = 8 * 64 / kThreads;  // row segments (16 columns of one token) per thread in L
+  // q, k rows as given (bf16, exact MFMA operands) with their l2norm factors; W and the lower
+  // tiles of P as hi | lo words with SPLIT, as bf16 (hi) without; g, e^g, e^{g_last - g}
+  using LW = std::conditional_t<SPLIT, uint32_t, uint16_t>;
+  constexpr int kWs = SPLIT ? kRs : kQs;     // W row stride, elements
+  constexpr int kPs2 = SPLIT ? kPs : kC + 8;  // P row stride, elements (bf16: 36 words, 8-byte reads conflict-free)
   __shared__ __attribute__((aligned(16))) uint16_t Ql[kC][kQs];
   __shared__ __attribute__((aligned(16))) uint16_t Kl[kC][kQs];
-  __shared__ __attribute__((aligned(16))) uint32_t Wl[kC][kRs];
-  __shared__ __attribute__((aligned(16))) uint32_t Pl[kC][kPs];
+  __shared__ __attribute__((aligned(16))) LW Wl[kC][kWs];
+  __shared__ __attribute__((aligned(16))) LW Pl[kC][kPs2];
   __shared__ float invq[kC], invk[kC];  // 1 / |q| / sqrt(D), 1 / |k| (eps 1e-6 inside the root)
   __shared__ float gl[kC], egl[kC], decl[kC];
   __shared__ float eglast;
@@ -174,48 +184,66 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
   }
 
   const Offsets of = offsets(a, b, h, t, wave, lane);
-  ChunkIn<WU_F32> in;
-  load_chunk<WU_F32>(a, of, 0, in);
+  ChunkIn<WU_F32, RP> in;
+  load_chunk<WU_F32, RP>(a, of, 0, in);
 
   auto chunk = [&](const int n) __attribute__((always_inline)) {
     // ---- L: q, k, W into LDS; norms; g, e^g, e^{g_last - g} ------------------------------------
-    {
-      const int row = t >> 3, seg = t & 7;
-      *reinterpret_cast<uint4 *>(&Ql[row][16 * seg]) = in.q[0];
-      *reinterpret_cast<uint4 *>(&Ql[row][16 * seg + 8]) = in.q[1];
-      *reinterpret_cast<uint4 *>(&Kl[row][16 * seg]) = in.k[0];
-      *reinterpret_cast<uint4 *>(&Kl[row][16 * seg + 8]) = in.k[1];
+#pragma unroll
+    for (int rp = 0; rp < RP; ++rp) {
+      const int row = (t >> 3) + 32 * rp, seg = t & 7;
+      *reinterpret_cast<uint4 *>(&Ql[row][16 * seg]) = in.q[rp][0];
+      *reinterpret_cast<uint4 *>(&Ql[row][16 * seg + 8]) = in.q[rp][1];
+      *reinterpret_cast<uint4 *>(&Kl[row][16 * seg]) = in.k[rp][0];
+      *reinterpret_cast<uint4 *>(&Kl[row][16 * seg + 8]) = in.k[rp][1];
       float f[16];
-      unbf16x8(in.q[0], f);
-      unbf16x8(in.q[1], f + 8);
+      unbf16x8(in.q[rp][0], f);
+      unbf16x8(in.q[rp][1], f + 8);
       float ss = 0.0f;
 #pragma unroll
       for (int x = 0; x < 16; ++x) ss = fmaf(f[x], f[x], ss);
       ss = sum8(ss);
       if (seg == 0) invq[row] = (1.0f / sqrtf(ss + 1e-6f)) * (1.0f / 11.313708498984761f);  // then 1/sqrt(128)
-      unbf16x8(in.k[0], f);
-      unbf16x8(in.k[1], f + 8);
+      unbf16x8(in.k[rp][0], f);
+      unbf16x8(in.k[rp][1], f + 8);
       ss = 0.0f;
 #pragma unroll
       for (int x = 0; x < 16; ++x) ss = fmaf(f[x], f[x], ss);
       ss = sum8(ss);
       if (seg == 0) invk[row] = 1.0f / sqrtf(ss + 1e-6f);
-      if constexpr (WU_F32) {
+      if constexpr (SPLIT) {
+        if constexpr (WU_F32) {
 #pragma unroll
-        for (int x = 0; x < 4; ++x)
-          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 4 * x]) =
-              make_uint4(hilo<SPLIT>(__uint_as_float(in.w[x].x)), hilo<SPLIT>(__uint_as_float(in.w[x].y)),
-                         hilo<SPLIT>(__uint_as_float(in.w[x].z)), hilo<SPLIT>(__uint_as_float(in.w[x].w)));
-      } else {  // bf16 W is exact: the hi part only
+          for (int x = 0; x < 4; ++x)
+            *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 4 * x]) =
+                make_uint4(hilo<SPLIT>(__uint_as_float(in.w[rp][x].x)), hilo<SPLIT>(__uint_as_float(in.w[rp][x].y)),
+                           hilo<SPLIT>(__uint_as_float(in.w[rp][x].z)), hilo<SPLIT>(__uint_as_float(in.w[rp][x].w)));
+        } else {  // bf16 W is exact: the hi part only
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const uint32_t w4[4] = {in.w[x].x, in.w[x].y, in.w[x].z, in.w[x].w};
-          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x]) =
-              make_uint4(w4[0] & 0xFFFFu, w4[0] >> 16, w4[1] & 0xFFFFu, w4[1] >> 16);
-          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x + 4]) =
-              make_uint4(w4[2] & 0xFFFFu, w4[2] >> 16, w4[3] & 0xFFFFu, w4[3] >> 16);
+          for (int x = 0; x < 2; ++x) {
+            const uint32_t w4[4] = {in.w[rp][x].x, in.w[rp][x].y, in.w[rp][x].z, in.w[rp][x].w};
+            *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x]) =
+                make_uint4(w4[0] & 0xFFFFu, w4[0] >> 16, w4[1] & 0xFFFFu, w4[1] >> 16);
+            *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x + 4]) =
+                make_uint4(w4[2] & 0xFFFFu, w4[2] >> 16, w4[3] & 0xFFFFu, w4[3] >> 16);
+          }
+        }
+      } else {  // bf16 LDS: W rounded to bf16 (a float32 W) or as given
+        if constexpr (WU_F32) {
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            const uint4 lo = in.w[rp][2 * x], hi = in.w[rp][2 * x + 1];
+            *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8 * x]) =
+                make_uint4(pack_bf16(__uint_as_float(lo.x), __uint_as_float(lo.y)), pack_bf16(__uint_as_float(lo.z), __uint_as_float(lo.w)),
+                           pack_bf16(__uint_as_float(hi.x), __uint_as_float(hi.y)), pack_bf16(__uint_as_float(hi.z), __uint_as_float(hi.w)));
+          }
+        } else {
+          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg]) = in.w[rp][0];
+          *reinterpret_cast<uint4 *>(&Wl[row][16 * seg + 8]) = in.w[rp][1];
         }
       }
+    }
+    {
       if (wave == 0) {
         const float g = scan64(in.gc);
         const float glast = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), 63));
@@ -235,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
     // Unconditional (the last chunk reloads itself, unused): behind a branch the compiler would
     // lose count of the loads in flight and make the next chunk wait for every memory operation,
     // this chunk's o stores included, instead of just these loads.
-    load_chunk<WU_F32>(a, of, min(n + 1, a.nchunks - 1), in);
+    load_chunk<WU_F32, RP>(a, of, min(n + 1, a.nchunks - 1), in);
 
     // ---- M: W S, q^ S, v_new; P tiles ----------------------------------------------------------
     Half4 sB[8];
@@ -249,10 +277,16 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
       const int c = 32 * p + 4 * qd;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t *wrow = Wl[16 * i + r16];
+        const LW *wrow = Wl[16 * i + r16];
         const uint16_t *qrow = Ql[16 * i + r16];
-        const Half4 w0 = unpack4(*reinterpret_cast<const uint4 *>(wrow + c));
-        const Half4 w1 = unpack4(*reinterpret_cast<const uint4 *>(wrow + c + 16));
+        Half4 w0, w1;
+        if constexpr (SPLIT) {
+          w0 = unpack4(*reinterpret_cast<const uint4 *>(wrow + c));
+          w1 = unpack4(*reinterpret_cast<const uint4 *>(wrow + c + 16));
+        } else {
+          w0 = bf16x4(wrow + c);
+          w1 = bf16x4(wrow + c + 16);
+        }
         ws[i] = WU_F32 ? mma<SPLIT>(w0, w1, sB[2 * p], sB[2 * p + 1], ws[i])
                        : mma_exact_a<SPLIT>(w0, w1, sB[2 * p], sB[2 * p + 1], ws[i]);
         qs[i] = mma_exact_a<SPLIT>(bf16x4(qrow + c), bf16x4(qrow + c + 16), sB[2 * p], sB[2 * p + 1], qs[i]);
@@ -268,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
         oacc[i][e] = qs[i][e] * (invq[row] * egl[row]);
       }
     }
-    for (int idx = wave; idx < 10; idx += 8) {  // wave-uniform
+    for (int idx = wave; idx < 10; idx += kThreads / 64) {  // wave-uniform
       int ti, tj;
       p_tile(idx, ti, tj);
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -285,7 +319,7 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
       for (int e = 0; e < 4; ++e) {
         const int row = 16 * ti + 4 * qd + e;
         const float pv = col <= row ? acc[e] * (invq[row] * kf) * expf(gl[row] - gl[col]) : 0.0f;
-        Pl[row][col] = hilo<SPLIT>(pv);
+        Pl[row][col] = static_cast<LW>(hilo<SPLIT>(pv));
       }
     }
     lds_barrier();
@@ -297,14 +331,20 @@ __global__ __launch_bounds__(kThreads) void gdn_state_kernel(StateArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v4f acc = oacc[i];
-      const uint32_t *prow = Pl[16 * i + r16];
+      const LW *prow = Pl[16 * i + r16];
 #pragma unroll
       for (int p = 0; p <= i / 2; ++p) {
         const bool two = 2 * p + 1 <= i;
         const int c = 32 * p + 4 * qd;
-        acc = mma<SPLIT>(unpack4(*reinterpret_cast<const uint4 *>(prow + c)),
-                         two ? unpack4(*reinterpret_cast<const uint4 *>(prow + c + 16)) : kZero4, vB[2 * p],
-                         two ? vB[2 * p + 1] : kZero4, acc);
+        Half4 p0, p1 = kZero4;
+        if constexpr (SPLIT) {
+          p0 = unpack4(*reinterpret_cast<const uint4 *>(prow + c));
+          if (two) p1 = unpack4(*reinterpret_cast<const uint4 *>(prow + c + 16));
+        } else {
+          p0 = bf16x4(prow + c);
+          if (two) p1 = bf16x4(prow + c + 16);
+        }
+        acc = mma<SPLIT>(p0, p1, vB[2 * p], two ? vB[2 * p + 1] : kZero4, acc);
       }
       if constexpr (OUT_F32) {
 #pragma unroll

@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kChThreads, 1) void qmm_chain_kernel(const ExactArg
   constexpr int D = A16 ? 2 : 1;       // activation digits
   constexpr int NP = W16 ? 2 : 1;      // weight planes
   constexpr int E = A16 ? 2 : 1;       // bytes per activation / output element
-  constexpr int kPitch = E * kChMaxK + 16;  // LDS row pitch: 16-byte skew per row spreads the banks
+  constexpr int kPitch = E * kChMaxK + 32;  // LDS row pitch: 8 (mod 16) dwords, so 16-byte fragment reads of 16 rows are conflict-free
   // the dividing contracts take the float64 path (bias_q is not part of them)
   constexpr bool kF64 = CT == QH_CONTRACT_DIV_RINT || CT == QH_CONTRACT_FLOOR256_DIV_RINT || CT == QH_CONTRACT_ROUND_DIV;
   __shared__ __align__(16) uint8_t buf[2][kChRows * kPitch];
