@@ -419,10 +419,14 @@ __global__ __launch_bounds__(kChThreads, 1) void qmm_chain_kernel(const ExactArg
   for (int i = t; i < kChRows * (kChMaxK * E / 16); i += kChThreads) {
     const int r = i / (kChMaxK * E / 16), c = i - r * (kChMaxK * E / 16);
     const int mr = min(m0 + r, g.M - 1);
-    const uint4 pad = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-    const uint4 v = 16 * c < rowb ? *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(mr) * rowb + 16 * c) : pad;
-    *reinterpret_cast<uint4 *>(&buf[0][r * kPitch + 16 * c]) = v;
-    if (16 * c >= rowb) *reinterpret_cast<uint4 *>(&buf[1][r * kPitch + 16 * c]) = pad;
+    constexpr uint32_t kPad = 0x80808080u;
+    const bool in = 16 * c < rowb;
+    // a clamped, always valid address and per-word selects (a select of whole uint4 values
+    // becomes a select of stack addresses, i.e. scratch memory)
+    const uint4 x = *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(mr) * rowb + 16 * min(c, rowb / 16 - 1));
+    *reinterpret_cast<uint4 *>(&buf[0][r * kPitch + 16 * c]) =
+        make_uint4(in ? x.x : kPad, in ? x.y : kPad, in ? x.z : kPad, in ? x.w : kPad);
+    if (!in) *reinterpret_cast<uint4 *>(&buf[1][r * kPitch + 16 * c]) = make_uint4(kPad, kPad, kPad, kPad);
   }
   // B fragments: lane holds 16 k (kg..kg+15 of each 64-k step) of column 32 w + 16 ct + lane % 16
   uint4 w[kChSteps][2][NP];
