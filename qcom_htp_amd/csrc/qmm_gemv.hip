@@ -46,6 +46,7 @@ struct GemvArgs {
   const uint8_t *w;      // GEMV stream
   const uint8_t *lpbq;   // block scales, gemv_scale_index layout
   const double *alpha, *beta, *margin, *absb, *bias_deq, *mr1, *mlo;
+  const double *alpha_e, *margin_exact;  // exact integer fixup (8-bit activations)
   const int64_t *corr, *mant, *colsum, *colsum_r;
   const float *s32;
   int M, N, K, KG, nbatch, sub_shift;
@@ -192,6 +193,94 @@ __device__ void gemv_fixup_batch(const GemvArgs &g, const uint8_t *lds, const ui
   }
 }
 
+// Exact integer completion of listed outputs, 8-bit activations, by the whole workgroup (one
+// output at a time).  With r_k = fl32(w_k M) - w_k M the float32 rounding residue of the
+// dequantised weight in units of 2^E (w_k the integer weight, block scale included; M 2^E the
+// column scale), D = sum_k (a_k - zp)(w_k M + r_k) = (sum_k a'_k w_k + corr) M + sum_k a'_k r_k
+// + (128 - zp) sum_k r_k is an exact integer, so t = D alpha_e + beta carries only the oracle's
+// own float64 noise (margin_exact).  Thread t takes the (k-group, half) pairs u = t, t + NT, ..
+// (terms k = 32 kg + 16 h + j, j < 16, as gemv_fixup_batch).  Outputs still within that noise of
+// a rounding boundary are moved to the front of the list for the term-by-term float64
+// recomputation; their count is returned (to every thread).
+template <int FMT, bool LPBQ, int NT>
+__device__ int gemv_fixup_exact(const GemvArgs &g, const uint8_t *lds, uint16_t *list, int nfix, int grp, int t,
+                                int (*ired)[NT / 64][2], int *cnt) {
+  constexpr int WB = FMT == kTileI4 ? 16 : 32;
+  const int KG = g.KG, lane = t & 63, wave = t >> 6;
+  int nslow = 0;  // thread 0's count
+  for (int e = 0; e < nfix; ++e) {
+    const int tt = list[e];
+    const int m = tt >> 4, n = grp * 16 + (tt & 15);
+    // column constants first (thread 0 uses them after the reduction)
+    const int Mi = static_cast<int>(g.mant[n]);
+    int64_t corr = 0, csr = 0;
+    double ae = 0.0, beta = 0.0, mex = 0.0, absb = 0.0;
+    if (t == 0) {
+      corr = g.corr[n];
+      csr = g.colsum_r[n];
+      ae = g.alpha_e[n];
+      beta = g.beta[n];
+      mex = g.margin_exact[n];
+      absb = g.absb[n];
+    }
+    const uint8_t *const wcol = g.w + (static_cast<size_t>(n / 16) * KG * 16 + (n % 16)) * WB;
+    int sw = 0, sr = 0;
+    for (int u = t; u < 2 * KG; u += NT) {
+      const int kg = u >> 1, h = u & 1;
+      const uint4 v = *reinterpret_cast<const uint4 *>(wcol + static_cast<size_t>(kg) * 16 * WB + (FMT == kTileI4 ? 0 : 16 * h));
+      const int f = LPBQ ? g.lpbq[gemv_scale_index_kg(n, kg, g.nbatch, g.sub_shift)] : 1;
+      const uint4 av = *reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(m) * g.ars + kg * 32 + 16 * h);
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w}, ad[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = (wd[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        const int w = FMT == kTileI4 ? (static_cast<int>(h ? (byte >> 4) : (byte & 15u)) - 8) * f : static_cast<int8_t>(byte);
+        const int a = static_cast<int8_t>((ad[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+        const int x = w * Mi;  // |w| <= 127, M < 2^24: no overflow
+        sw += a * w;
+        sr += a * (static_cast<int>(static_cast<float>(x)) - x);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      sw += __shfl_xor(sw, o, 64);
+      sr += __shfl_xor(sr, o, 64);
+    }
+    if (lane == 0) {
+      ired[e & 1][wave][0] = sw;
+      ired[e & 1][wave][1] = sr;
+    }
+    lds_barrier();  // (double-buffered: iteration e + 2 rewrites this slot after the next barrier)
+    if (t == 0) {
+      int64_t SW = 0, SR = 0;
+#pragma unroll
+      for (int w = 0; w < NT / 64; ++w) {
+        SW += ired[e & 1][w][0];
+        SR += ired[e & 1][w][1];
+      }
+      const int64_t D = (SW + corr) * static_cast<int64_t>(Mi) + SR + static_cast<int64_t>(128 - g.act_zp) * csr;
+      const double tv = fma(static_cast<double>(D), ae, beta);
+      const double slack = mex + 0x1p-48 * (fabs(tv) + absb);
+      const double fl = floor(tv);
+      const double lo = fmin(fmax(fl, 0.0), static_cast<double>(g.out_qmax));
+      const double hi = fmin(fmax(fl + 1.0, 0.0), static_cast<double>(g.out_qmax));
+      if (fabs((tv - fl) - 0.5) <= slack && lo != hi) {
+        list[nslow++] = static_cast<uint16_t>(tt);  // every thread has read entries <= e
+      } else {
+        const double o = fmin(fmax(rint(tv), 0.0), static_cast<double>(g.out_qmax));
+        const size_t idx = static_cast<size_t>(m) * g.N + n;
+        if (g.out16)
+          static_cast<uint16_t *>(g.out)[idx] = static_cast<uint16_t>(o);
+        else
+          static_cast<uint8_t *>(g.out)[idx] = static_cast<uint8_t>(o);
+      }
+    }
+  }
+  if (t == 0) *cnt = nslow;
+  lds_barrier();
+  return *cnt;
+}
+
 // Staging of the activations, one (row, k-group) unit of 32 values at a time: the signed
 // plane bytes and (int4 weights) the plane sums over the unit.  16-bit activations also add
 // sum |a - zp| of each row into r1 (the bound of the float32-rounding residue term in the
@@ -293,6 +382,7 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
   __shared__ uint16_t fix_list[MM * 16];
   __shared__ int fix_cnt;
   __shared__ double dred[kFixBatch * kGemvWaves];
+  __shared__ int ired[A16 ? 1 : 2][A16 ? 1 : NT / 64][2];
 
   const int t = threadIdx.x, lane = t & 63;
   // the wave of the lane pattern (k-groups 4 (wave + 4 i) + sub) and, 8 waves, the half of the
@@ -657,8 +747,13 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
     lds_barrier();
     const int nfix = fix_cnt;
     if (kLoop || KG > kGemvBatchKG) {
-      // the weight registers hold the next group or only the last batch: re-read the column
-      for (int e = t >> 6; e < nfix; e += NT / 64) {
+      // the weight registers hold the next group or only the last batch: re-read the column.
+      // 8-bit activations complete the residue term exactly first; what stays ambiguous (within
+      // the oracle's own float noise of a rounding boundary) is recomputed term by term.
+      int nslow = nfix;
+      if constexpr (!A16)
+        if (nfix > 0) nslow = gemv_fixup_exact<FMT, LPBQ, NT>(g, lds, fix_list, nfix, grp, t, ired, &fix_cnt);
+      for (int e = t >> 6; e < nslow; e += NT / 64) {
         const int tt = fix_list[e];
         gemv_fixup<A16, FMT, LPBQ>(g, lds, tt >> 4, grp * 16 + (tt & 15), lane);
       }
@@ -829,6 +924,8 @@ qh_status launch_qmm_gemv(const qh_qmm_prepared *p, int m, const void *act, void
   g.mant = D.mant;
   g.colsum = D.colsum;
   g.colsum_r = D.colsum_r;
+  g.alpha_e = D.alpha_e;
+  g.margin_exact = D.margin_exact;
   g.s32 = D.s32;
   g.M = m;
   g.N = sh.N;

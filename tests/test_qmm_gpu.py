@@ -232,6 +232,34 @@ def test_near_tie_outputs_bit_exact(gpu, fam):
     assert np.array_equal(got, want[:16]), f"gemv: {diff_msg(got, want[:16])}"
 
 
+@pytest.mark.parametrize("fam", ["u8i8", "w4a8_per_channel", "w4a8_lpbq"])
+@pytest.mark.parametrize("k", [512, 8192])
+@pytest.mark.parametrize("rows", [1, 6, 16])
+def test_gemv_exact_ties_bit_exact(gpu, fam, k, rows):
+    """Power-of-two scales make every weight product exact (zero rounding residues) and the
+    output scale puts odd integer dot products exactly half way between two outputs: the exact
+    integer completion of 8-bit-activation outputs cannot settle them, so they take the
+    term-by-term float64 recomputation, which rounds them half to even as the oracle does."""
+    import dataclasses
+
+    c = C.synthetic_case(fam, 16, k, 96, seed=43)
+    rng = np.random.default_rng(44)
+    zp = c.family.act_zp
+    x = np.full_like(c.activation_q, zp)
+    for r in range(16):
+        pos = rng.choice(k, size=5, replace=False)
+        x[r, pos] = zp + rng.integers(-3, 4, size=5)
+    sA, sg = 2.0 ** -7, 2.0 ** -8
+    w_int = c.lpbq_expanded_q_nk if c.lpbq_expanded_q_nk is not None else c.weight_q_nk
+    c = dataclasses.replace(c, activation_q=x, act_scale=sA, weight_scale=np.full(96, sg, np.float32),
+                            out_scale=2.0 * sA * sg, bias_q=rng.integers(-8, 8, size=96).astype(np.int32),
+                            weight_deq=w_int.astype(np.float32) * np.float32(sg))
+    want = oq.expected_output_case(c)[:rows]
+    print(f"[qmm] {fam} exact-tie gemv rows={rows} k={k}", flush=True)
+    got = run(c, gpu, path=2, rows=rows)
+    assert np.array_equal(got, want), f"gemv: {diff_msg(got, want)}"
+
+
 @pytest.mark.parametrize("fam", C.GATED_FAMILIES)
 @pytest.mark.parametrize("k", [512, 8192])
 @pytest.mark.parametrize("rows", [1, 4, 6, 16])
