@@ -64,11 +64,12 @@ __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
 
 // Exact float64 recomputation of output (m, n) by a whole wave, term by term as the reference
 // oracle forms it: sum_k fl64((a_k - zp) * sA) * fl32(w_k * s32), + bias_deq, / sO, + out_zp.
-// The activations come from the staged LDS planes.
+// The activations come from the staged LDS planes, or (GA, 8-bit) from the activation matrix.
 // Kept lean on purpose: the kernel's register budget is the maximum over all of its code, and
 // this rare path must not lower the occupancy of the stream.
-template <bool A16, int FMT, bool LPBQ>
+template <bool A16, int FMT, bool LPBQ, bool GA = false>
 __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, int lane) {
+  static_assert(!GA || !A16, "activations are read from global memory for 8-bit rows only");
   constexpr int WB = FMT == kTileI4 ? 16 : 32;
   const float sc = g.s32[n];
   const int KG = g.KG;
@@ -100,6 +101,7 @@ __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, 
       const int f = fs[u];
       const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
       const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * g.ars + kg * 32);
+      const uint8_t *gp = g.act + static_cast<size_t>(m) * g.K + kg * 32;
 #pragma unroll 4
       for (int j = 0; j < 32; ++j) {
         int w;
@@ -109,7 +111,7 @@ __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, 
         } else {
           w = static_cast<int8_t>((wd[u][j >> 2] >> (8 * (j & 3))) & 0xFFu);
         }
-        const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : static_cast<int>(hp[j])) + off;
+        const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : (GA ? static_cast<int>(gp[j]) - 128 : static_cast<int>(hp[j]))) + off;
         const float wf = static_cast<float>(w) * sc;
         s = fma(static_cast<double>(a) * g.sA, static_cast<double>(wf), s);
       }
@@ -201,8 +203,9 @@ __device__ void gemv_fixup_batch(const GemvArgs &g, const uint8_t *lds, const ui
 // own float64 noise (margin_exact).  Thread t takes the (k-group, half) pairs u = t, t + NT, ..
 // (terms k = 32 kg + 16 h + j, j < 16, as gemv_fixup_batch).  Outputs still within that noise of
 // a rounding boundary are moved to the front of the list for the term-by-term float64
-// recomputation; their count is returned (to every thread).
-template <int FMT, bool LPBQ, int NT>
+// recomputation; their count is returned (to every thread).  GA: the activations are read from
+// the activation matrix instead of the staged plane.
+template <int FMT, bool LPBQ, int NT, bool GA>
 __device__ int gemv_fixup_exact(const GemvArgs &g, const uint8_t *lds, uint16_t *list, int nfix, int grp, int t,
                                 int (*ired)[NT / 64][2], int *cnt) {
   constexpr int WB = FMT == kTileI4 ? 16 : 32;
@@ -229,7 +232,13 @@ __device__ int gemv_fixup_exact(const GemvArgs &g, const uint8_t *lds, uint16_t 
       const int kg = u >> 1, h = u & 1;
       const uint4 v = *reinterpret_cast<const uint4 *>(wcol + static_cast<size_t>(kg) * 16 * WB + (FMT == kTileI4 ? 0 : 16 * h));
       const int f = LPBQ ? g.lpbq[gemv_scale_index_kg(n, kg, g.nbatch, g.sub_shift)] : 1;
-      const uint4 av = *reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(m) * g.ars + kg * 32 + 16 * h);
+      uint4 av;
+      if constexpr (GA) {
+        av = *reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(m) * g.K + kg * 32 + 16 * h);
+        av.x ^= 0x80808080u; av.y ^= 0x80808080u; av.z ^= 0x80808080u; av.w ^= 0x80808080u;
+      } else {
+        av = *reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(m) * g.ars + kg * 32 + 16 * h);
+      }
       const uint32_t wd[4] = {v.x, v.y, v.z, v.w}, ad[4] = {av.x, av.y, av.z, av.w};
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -361,8 +370,12 @@ constexpr int gemv_threads() {
   return MM == 16 && A16 ? 2 * kGemvThreads : kGemvThreads;
 }
 
-template <bool A16, int FMT, bool LPBQ, int MM>
+// RA (8-bit activations, 16 rows, K <= 16 kU k-groups): every lane keeps the A operands of its
+// slots in registers, loaded once from the activation matrix (the same for every group the
+// workgroup takes), instead of staging the rows in LDS.
+template <bool A16, int FMT, bool LPBQ, int MM, bool RA = false>
 __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2) : 4)) void qmm_gemv_kernel(const GemvArgs g) {
+  static_assert(!RA || (!A16 && MM == 16), "register-held activations: 8-bit activations, 16 rows");
   constexpr int NT = gemv_threads<A16, MM>();
   constexpr bool kWide = NT > kGemvThreads;
   constexpr int kUw = kWide ? kU / 2 : kU;  // slots of a batch per wave
@@ -467,7 +480,31 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
   // per thread and no registers to spare under their occupancy bound
   constexpr int kStageB = MM < 16 ? 1 : (A16 ? 4 : 8);
   int ustart = t + NT;  // the first unit of the staging loop below
-  if constexpr (kLoop) {
+  uint4 areg[RA ? kU : 1][2];  // RA: activation row lane % 16, k-group of slot i (32 bytes)
+  if constexpr (RA) {
+    // the activation fragments first (L2: every workgroup reads the same rows), then the
+    // per-group constants and the first group's weights (HBM)
+    const int arow = min(lane & 15, M - 1);  // rows past M repeat row M - 1 (never stored)
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+      const int kg = min(4 * (wave + 4 * i) + sub, KG - 1);
+      const uint4 *p = reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(arow) * g.K + kg * 32);
+      areg[i][0] = p[0];
+      areg[i][1] = p[1];
+    }
+    load_epi(blockIdx.x);
+    issue(blockIdx.x, 0);
+    if (t < 16) r1[t] = 0;
+    if (t == 0) fix_cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kU; ++i)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        areg[i][q].x ^= 0x80808080u; areg[i][q].y ^= 0x80808080u;
+        areg[i][q].z ^= 0x80808080u; areg[i][q].w ^= 0x80808080u;
+      }
+    ustart = units;  // nothing to stage
+  } else if constexpr (kLoop) {
     // 16 rows: the staged activations (L2) are requested first, then the per-group constants
     // and the first group's weights (HBM): one counter tracks the loads in order, so the staging
     // waits for its own loads only and overlaps the weights' latency.
@@ -530,7 +567,8 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
       if (HR && !kMfma) acc3[m] = 0;
     }
     v4i macc = {0, 0, 0, 0}, macc2 = {0, 0, 0, 0}, macc3 = {0, 0, 0, 0}, macc4 = {0, 0, 0, 0};
-    for (int i0 = 0; i0 < iters; i0 += kU) {
+    // (RA: the host guarantees one batch, iters <= kU)
+    for (int i0 = 0; i0 < (RA ? 1 : iters); i0 += kU) {
       if (i0 > 0) issue(grp, i0);
       if constexpr (kMfma) {
         // 16 rows: v_mfma_i32_16x16x32_i8 over the k-groups of the wave's 4 lane quarters.  In
@@ -568,8 +606,15 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
             b[4] = v1.x & mk; b[5] = v1.y & mk; b[6] = v1.z & mk; b[7] = v1.w & mk;
           }
           // 16-byte reads: with the padded row stride the 16 rows of a quarter hit distinct banks
-          const uint4 *ap4 = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(mrow) * g.ars + kg * 32);
-          const uint4 ah0 = ap4[0], ah1 = ap4[1];
+          uint4 ah0, ah1;
+          if constexpr (RA) {
+            ah0 = areg[ii][0];
+            ah1 = areg[ii][1];
+          } else {
+            const uint4 *ap4 = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(mrow) * g.ars + kg * 32);
+            ah0 = ap4[0];
+            ah1 = ap4[1];
+          }
           const uint2 ah[4] = {make_uint2(ah0.x, ah0.y), make_uint2(ah0.z, ah0.w), make_uint2(ah1.x, ah1.y), make_uint2(ah1.z, ah1.w)};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
@@ -752,10 +797,10 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
       // the oracle's own float noise of a rounding boundary) is recomputed term by term.
       int nslow = nfix;
       if constexpr (!A16)
-        if (nfix > 0) nslow = gemv_fixup_exact<FMT, LPBQ, NT>(g, lds, fix_list, nfix, grp, t, ired, &fix_cnt);
+        if (nfix > 0) nslow = gemv_fixup_exact<FMT, LPBQ, NT, RA>(g, lds, fix_list, nfix, grp, t, ired, &fix_cnt);
       for (int e = t >> 6; e < nslow; e += NT / 64) {
         const int tt = fix_list[e];
-        gemv_fixup<A16, FMT, LPBQ>(g, lds, tt >> 4, grp * 16 + (tt & 15), lane);
+        gemv_fixup<A16, FMT, LPBQ, RA>(g, lds, tt >> 4, grp * 16 + (tt & 15), lane);
       }
     } else {
       // the column's weights (one batch: K <= 4096) are still in the registers of its 16
@@ -793,9 +838,9 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
 // driver round trip, too much for a launch that streams 30 MB in a few microseconds).  The
 // cache is keyed by the instantiation's template arguments: every instantiation has the same
 // function type, so a cache keyed by that type would be shared by all of them.
-template <bool A16, int FMT, bool LPBQ, int MM>
+template <bool A16, int FMT, bool LPBQ, int MM, bool RA = false>
 qh_status allow_dyn_lds() {
-  const auto kernel = &qmm_gemv_kernel<A16, FMT, LPBQ, MM>;
+  const auto kernel = &qmm_gemv_kernel<A16, FMT, LPBQ, MM, RA>;
   static std::atomic<uint32_t> done{0};  // bit d: set on device d
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -809,11 +854,11 @@ qh_status allow_dyn_lds() {
   return QH_STATUS_OK;
 }
 
-template <bool A16, int FMT, bool LPBQ, int MM>
+template <bool A16, int FMT, bool LPBQ, int MM, bool RA = false>
 qh_status launch_one(const GemvArgs &g, dim3 grid, size_t dyn_lds, hipStream_t stream) {
-  const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, MM>();
+  const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, MM, RA>();
   if (st != QH_STATUS_OK) return st;
-  hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MM>), grid, dim3(gemv_threads<A16, MM>()), dyn_lds, stream, g);
+  hipLaunchKernelGGL((qmm_gemv_kernel<A16, FMT, LPBQ, MM, RA>), grid, dim3(gemv_threads<A16, MM>()), dyn_lds, stream, g);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "qmm_gemv_kernel launch");
   return QH_STATUS_OK;
@@ -821,7 +866,7 @@ qh_status launch_one(const GemvArgs &g, dim3 grid, size_t dyn_lds, hipStream_t s
 
 // Workgroups of the 16-row kernel that are resident at once with dyn_lds bytes of dynamic LDS
 // (occupancy x compute units), or 0 if the runtime cannot say.  Cached for the last query.
-template <bool A16, int FMT, bool LPBQ>
+template <bool A16, int FMT, bool LPBQ, bool RA>
 int resident_workgroups(size_t dyn_lds) {
   static std::atomic<uint64_t> last{0};  // dyn_lds << 24 | device << 16 | workgroups
   int dev = 0;
@@ -830,7 +875,7 @@ int resident_workgroups(size_t dyn_lds) {
   const uint64_t hit = last.load(std::memory_order_acquire);
   if ((hit & ~static_cast<uint64_t>(0xFFFF)) == key && (hit & 0xFFFF) != 0) return static_cast<int>(hit & 0xFFFF);
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(&qmm_gemv_kernel<A16, FMT, LPBQ, 16>),
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(&qmm_gemv_kernel<A16, FMT, LPBQ, 16, RA>),
                                                    gemv_threads<A16, 16>(), dyn_lds) != hipSuccess)
     return 0;
   const long long wg = static_cast<long long>(occ) * device_cu_count();
@@ -839,21 +884,20 @@ int resident_workgroups(size_t dyn_lds) {
   return static_cast<int>(wg);
 }
 
-template <bool A16, int FMT, bool LPBQ>
-qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
+// Workgroups of a 16-row launch: one group each while the staged activations are small.  Larger
+// staging is amortised over several groups per workgroup: at most 512 workgroups, and no more
+// than are resident at once, since a second round would stage the activations again (16 rows of
+// 16-bit activations at K = 4096 take 128 KiB, one workgroup per compute unit).  Register-held
+// activations follow the same rule: each workgroup reads the rows once.
+template <bool A16, int FMT, bool LPBQ, bool RA>
+qh_status launch_16(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
   const int groups = g.N / 16;
-  // One group per workgroup while the staged activations are small.  Larger staging is
-  // amortised over several groups per workgroup: at most 512 workgroups, and no more than are
-  // resident at once, since a second round would stage the activations again (16 rows of
-  // 16-bit activations at K = 4096 take 128 KiB, one workgroup per compute unit).
-  if (g.M <= 1) return launch_one<A16, FMT, LPBQ, 1>(g, dim3(groups), dyn_lds, stream);
-  if (g.M <= 4) return launch_one<A16, FMT, LPBQ, 4>(g, dim3(groups), dyn_lds, stream);
   const int planes = A16 ? 2 : 1;
   int blocks = groups;
   if (static_cast<size_t>(planes) * g.M * g.K > 16384) {
-    const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, 16>();  // before the occupancy query
+    const qh_status st = allow_dyn_lds<A16, FMT, LPBQ, 16, RA>();  // before the occupancy query
     if (st != QH_STATUS_OK) return st;
-    const int cap = resident_workgroups<A16, FMT, LPBQ>(dyn_lds);
+    const int cap = resident_workgroups<A16, FMT, LPBQ, RA>(dyn_lds);
     const int lim = cap > 0 && cap < 512 ? cap : 512;
     if (blocks > lim) {
       // the same number of groups per workgroup (rounded up), so the workgroups end together
@@ -861,7 +905,18 @@ qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
       blocks = (groups + per - 1) / per;
     }
   }
-  return launch_one<A16, FMT, LPBQ, 16>(g, dim3(blocks), dyn_lds, stream);
+  return launch_one<A16, FMT, LPBQ, 16, RA>(g, dim3(blocks), dyn_lds, stream);
+}
+
+template <bool A16, int FMT, bool LPBQ>
+qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
+  const int groups = g.N / 16;
+  if (g.M <= 1) return launch_one<A16, FMT, LPBQ, 1>(g, dim3(groups), dyn_lds, stream);
+  if (g.M <= 4) return launch_one<A16, FMT, LPBQ, 4>(g, dim3(groups), dyn_lds, stream);
+  // 8-bit rows whose k-groups fit one batch per lane (K <= 16 kU x 32) stay in registers
+  if constexpr (!A16)
+    if (g.KG <= 16 * kU) return launch_16<A16, FMT, LPBQ, true>(g, 0, stream);
+  return launch_16<A16, FMT, LPBQ, false>(g, dyn_lds, stream);
 }
 
 size_t align16(size_t x) { return (x + 15) & ~static_cast<size_t>(15); }
