@@ -67,6 +67,23 @@ def time_kernel(fn, steps: int, warmup: int):
     return wall, ev
 
 
+def time_graph(launch, steps: int, warmup: int):
+    """(ms per step, wall clock; ms per step, stream events) of one replay of a HIP graph that holds
+    `steps` launches, captured after `warmup` eager launches: the GPU runs the kernels back to back,
+    without the gaps of launches issued one by one from Python.  (Capturing runs nothing.)"""
+    import torch
+
+    for _ in range(warmup):
+        launch(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            launch(i)
+    wall, ev = time_kernel(lambda i: graph.replay(), 1, 0)
+    return wall / steps, ev / steps
+
+
 def parity_check(case, got) -> dict:
     """Every output of the timed launches against the oracle (after the timed region)."""
     import numpy as np
@@ -91,9 +108,13 @@ def gemm_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     op = QuantMatmul.from_case(case, device=dev)
     act = torch.from_numpy(case.activation_q).to(dev)
     out = torch.empty((m, n), dtype=op.out_dtype, device=dev)
-    wall, ev = time_kernel(lambda i: op(act, out=out, path=PATH_GEMM), steps, warmup)
+    launch = lambda i: op(act, out=out, path=PATH_GEMM)
+    wall, ev = time_graph(launch, steps, warmup)
+    wall_e, ev_e = time_kernel(launch, steps, 0)  # the same launches issued from Python, after the timed ones
     ops = 2.0 * m * k * n
-    res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "tops": ops / (ev * 1e-3) / 1e12}
+    res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "tops": ops / (ev * 1e-3) / 1e12,
+           "eager_ms": ev_e, "eager_tops": ops / (ev_e * 1e-3) / 1e12,
+           "timing": f"one replay of a HIP graph holding the {steps} timed launches (stream events); eager_ms: the same launches issued from Python"}
     res.update(parity_check(case, out.cpu().numpy()))
     op.close()
     return res, case
@@ -114,9 +135,12 @@ def gemm_rotated_workload(family: str, m: int, k: int, n: int, steps: int, warmu
     act0 = torch.from_numpy(case.activation_q).to(dev)
     acts = [act0.clone() for _ in range(copies)]
     outs = [torch.empty((m, n), dtype=ops[0].out_dtype, device=dev) for _ in range(copies)]
-    wall, ev = time_kernel(lambda i: ops[i % copies](acts[i % copies], out=outs[i % copies], path=PATH_GEMM), steps, warmup)
+    launch = lambda i: ops[i % copies](acts[i % copies], out=outs[i % copies], path=PATH_GEMM)
+    wall, ev = time_graph(launch, steps, warmup)
+    wall_e, ev_e = time_kernel(launch, steps, 0)
     torch.cuda.synchronize()
     res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "tops": 2.0 * m * k * n / (ev * 1e-3) / 1e12,
+           "eager_ms": ev_e, "eager_tops": 2.0 * m * k * n / (ev_e * 1e-3) / 1e12,
            "copies": copies, "rotated_mb": copies * (k * n + m * k) / 1e6}  # int8 weight tiles + activations
     res.update(parity_check(case, outs[0].cpu().numpy()))
     same = all(torch.equal(outs[0], o) for o in outs[1:])
@@ -204,7 +228,9 @@ def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
     dev = torch.device("cuda", 0)
     a = torch.from_numpy(A.astype(np.float32)).to(dev)
     out = torch.empty_like(a)
-    wall, ev = time_kernel(lambda i: gdn_solve(a, precision=precision, out=out), steps, warmup)
+    launch = lambda i: gdn_solve(a, precision=precision, out=out)
+    wall, ev = time_graph(launch, steps, warmup)  # a solve is about as short as its launch from Python
+    wall_e, ev_e = time_kernel(launch, steps, 0)
     flops = (2.0 / 3.0) * C ** 3 * heads
     from oracle import gdn as og  # the checker
 
@@ -213,7 +239,8 @@ def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
     if not err <= tol:
         raise RuntimeError(f"GDN solve C={C} precision={precision}: oc {err:.3e} > {tol:.1e}")
     return {"heads": heads, "C": C, "precision": "fp32" if precision == 0 else "bf16", "ms": ev, "wall_ms": wall,
-            "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12, "oc_vs_fp64": err}, A
+            "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12, "oc_vs_fp64": err,
+            "eager_ms": ev_e, "timing": "graph replay of the timed launches; eager_ms: issued one by one"}, A
 
 
 def gdn_chunk_workload(B: int, T: int, H: int, C: int, steps: int, warmup: int):
@@ -376,7 +403,9 @@ def gdn_u16_workload(heads: int, C: int, steps: int, warmup: int, precision: int
     dev = torch.device("cuda", 0)
     a = torch.from_numpy(codes.view(np.int16)).to(dev).view(torch.uint16)
     out = torch.empty_like(a)
-    wall, ev = time_kernel(lambda i: GdnSolve(a, 32768, sA, 32768, sT, precision=precision, out=out), steps, warmup)
+    launch = lambda i: GdnSolve(a, 32768, sA, 32768, sT, precision=precision, out=out)
+    wall, ev = time_graph(launch, steps, warmup)
+    wall_e, ev_e = time_kernel(launch, steps, 0)
     Ad = (codes.astype(np.int64) - 32768) * sA
     Td = (out.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.int64) - 32768) * sT
     err = og.oc(Td, og.inverse_fp64(Ad))
@@ -385,7 +414,7 @@ def gdn_u16_workload(heads: int, C: int, steps: int, warmup: int, precision: int
     flops = (2.0 / 3.0) * C ** 3 * heads
     return {"heads": heads, "C": C, "precision": "fp32" if precision == 0 else "bf16", "ms": ev, "wall_ms": wall,
             "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12, "oc_vs_fp64": err,
-            "sA": sA, "sT": sT, "zp": 32768}
+            "eager_ms": ev_e, "sA": sA, "sT": sT, "zp": 32768}
 
 
 def cpu_baseline(case, gdn_A):
@@ -510,9 +539,16 @@ def vendor_int8_gemm_workload(M: int, K: int, N: int, steps: int, warmup: int):
     a = torch.randint(-128, 128, (M, K), dtype=torch.int8, device="cuda", generator=g)
     b = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
     bt = b.t()
-    wall, ev = time_kernel(lambda i: torch._int_mm(a, bt), steps, warmup)
+    try:  # timed like the GEMM lines: one replay of a graph of the timed launches
+        wall, ev = time_graph(lambda i: torch._int_mm(a, bt), steps, warmup)
+        how = "graph replay"
+    except Exception as e:  # the library may refuse capture: eager only
+        log(f"vendor GEMM graph capture failed ({e}); eager timing")
+        torch.cuda.synchronize()
+        wall, ev, how = *time_kernel(lambda i: torch._int_mm(a, bt), steps, warmup), "eager"
+    wall_e, ev_e = time_kernel(lambda i: torch._int_mm(a, bt), steps, 0)
     return {"m": M, "k": K, "n": N, "ms": ev, "wall_ms": wall, "tops": 2.0 * M * K * N / (ev * 1e-3) / 1e12,
-            "what": "torch._int_mm (i8 x i8 -> i32, no requantisation)"}
+            "eager_ms": ev_e, "timing": how, "what": "torch._int_mm (i8 x i8 -> i32, no requantisation)"}
 
 
 def lpbq_expand_workload(k: int, n: int, steps: int, warmup: int):
@@ -615,7 +651,8 @@ def main() -> int:
                    "m": M, "k": K, "n": N, "family": "w4a8_per_channel"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": I8_PEAK_TOPS, "unit": "TOPS",
                      "frac": round(tops / I8_PEAK_TOPS, 4), "traffic": measured_traffic("w4a8_gemm_4096"),
-                     "kernel": "qmm_gemm_kernel<A8> (int8 weight tiles)", "measured": "stream events over the timed steps"},
+                     "kernel": "qmm_gemm_kernel<A8> (int8 weight tiles)",
+                     "measured": "stream events over one replay of a HIP graph of the timed steps"},
         "extra": extra,
     }
     if not args.quick and not args.only:
