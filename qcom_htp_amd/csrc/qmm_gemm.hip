@@ -179,7 +179,13 @@ __device__ __forceinline__ int wave_sum(int v) {
          __builtin_amdgcn_readlane(v, 48);
 }
 
-__device__ __forceinline__ int clamp_out(int v, int qmax) { return min(max(v, 0), qmax); }
+// min(max(v, 0), qmax) in one instruction: the median of (v, 0, qmax) for qmax >= 0 (the compiler
+// forms v_med3_i32 only for compile-time bounds).
+__device__ __forceinline__ int clamp_out(int v, int qmax) {
+  int r;
+  asm("v_med3_i32 %0, %1, 0, %2" : "=v"(r) : "v"(v), "s"(qmax));
+  return r;
+}
 
 // rint(t) without the float64 round / convert instructions: adding 1.5 * 2^52 leaves the
 // rounded integer (ties to even) in the low word, exact for |t| < 2^31.  CLAMP first limits t
@@ -650,7 +656,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
           static_for<4>([&](auto jj) {
             const double tv = fma(static_cast<double>(acc[mt][nt][4 * decltype(jg)::value + decltype(jj)::value]), alpha, beta);
             int oi;
-            dmax = fmax(dmax, round_near<CLAMP>(tv, qmaxd, &oi));
+            const double d = round_near<CLAMP>(tv, qmaxd, &oi);
+            dmax = decltype(jj)::value == 0 ? d : fmax(dmax, d);
             o[jj] = clamp_out(oi, g.out_qmax);
           });
           if (dmax > thr) {  // rare: list the uncertain outputs of the strip with their sums
@@ -698,7 +705,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
           double dmax = 0.0;
           static_for<4>([&](auto jj) {
             int oi;
-            dmax = fmax(dmax, round_near<CLAMP>(t_of(jj), qmaxd, &oi));
+            const double d = round_near<CLAMP>(t_of(jj), qmaxd, &oi);
+            dmax = decltype(jj)::value == 0 ? d : fmax(dmax, d);
             o[jj] = clamp_out(oi, g.out_qmax);
           });
           if (dmax > thr) {  // rare: list the uncertain outputs of the strip with their sums
