@@ -130,23 +130,56 @@ __device__ __forceinline__ void load_w16(const GemmArgs g, int cb, int k, int (&
   for (int j = 0; j < 16; ++j) w[j] = b[j];
 }
 
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+// Buffer resource over the rows of one tile's output that lie below M.  A store at an offset
+// past them is dropped by the hardware range check, so the epilogue tests no row.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// R * pitch for a compile-time row step R, as one scalar multiply (left to itself the compiler
+// folds the uniform product into a per-lane 64-bit multiply-add).
+template <int R>
+__device__ __forceinline__ uint32_t row_step(uint32_t pitch) {
+  if constexpr (R == 0) {
+    return 0u;
+  } else {
+    uint32_t r;
+    asm("s_mul_i32 %0, %1, %2" : "=s"(r) : "s"(pitch), "i"(R));
+    return r;
+  }
+}
+
+// Per-lane constants of the quad exchange in store_strip (lane q of its quad).
+struct StripLane {
+  uint32_t sel;  // byte (8-bit outputs) or half-word (16-bit outputs) select of row q
+  bool upper;    // 16-bit outputs: the lane stores the second pair of rows' words
+};
+template <bool OUT16>
+__device__ __forceinline__ StripLane strip_lane(int q) {
+  if (!OUT16) return {static_cast<uint32_t>(q) | (static_cast<uint32_t>(4 + q) << 8) | 0x0C0C0000u, false};
+  return {(q & 1) ? 0x07060302u : 0x05040100u, q >= 2};
+}
+
 // Lane q of a quad holds outputs o[0..3] of tile rows R..R+3 in its own column; the quad
-// exchanges them (DPP quad broadcasts + byte permutes) so that lane q stores tile row
-// row = R + q, tile columns col..col+3 (4 adjacent outputs in one store).
-__device__ __forceinline__ void store_strip(const GemmArgs &g, uint8_t *tile_out, int m0, int n0, int row, int col,
-                                            const int (&o)[4], int q, bool full) {
-  const bool ok = full || (m0 + row < g.M && n0 + col < g.N);
-  const uint32_t off = static_cast<uint32_t>(row) * static_cast<uint32_t>(g.N) + static_cast<uint32_t>(col);
-  if (!g.out16) {
-    const uint32_t p = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 8) |
-                       (static_cast<uint32_t>(o[2]) << 16) | (static_cast<uint32_t>(o[3]) << 24);
+// exchanges them (DPP quad broadcasts + byte permutes) so that lane q stores tile row R + q,
+// tile columns col..col+3 (4 adjacent outputs in one store) at byte offset off of the tile's
+// output (an offset at or past the resource's end for a row past M or a column past N).
+template <bool OUT16>
+__device__ __forceinline__ void store_strip(__amdgpu_buffer_rsrc_t r, uint32_t off, const int (&o)[4], const StripLane &sl) {
+  if constexpr (!OUT16) {
+    // outputs are clamped to [0, 255]: three byte permutes pack them (the compiler's shift / or
+    // form takes four instructions)
+    const uint32_t lo = perm(static_cast<uint32_t>(o[1]), static_cast<uint32_t>(o[0]), 0x0C0C0400u);
+    const uint32_t hi = perm(static_cast<uint32_t>(o[3]), static_cast<uint32_t>(o[2]), 0x0C0C0400u);
+    const uint32_t p = perm(hi, lo, 0x05040100u);
     const uint32_t x0 = __builtin_amdgcn_mov_dpp(p, 0x00, 0xF, 0xF, false);
     const uint32_t x1 = __builtin_amdgcn_mov_dpp(p, 0x55, 0xF, 0xF, false);
     const uint32_t x2 = __builtin_amdgcn_mov_dpp(p, 0xAA, 0xF, 0xF, false);
     const uint32_t x3 = __builtin_amdgcn_mov_dpp(p, 0xFF, 0xF, 0xF, false);
-    const uint32_t sel = static_cast<uint32_t>(q) | (static_cast<uint32_t>(4 + q) << 8) | 0x0C0C0000u;
-    const uint32_t w = perm(perm(x3, x2, sel), perm(x1, x0, sel), 0x05040100u);
-    if (ok) *reinterpret_cast<uint32_t *>(tile_out + off) = w;
+    const uint32_t w = perm(perm(x3, x2, sl.sel), perm(x1, x0, sl.sel), 0x05040100u);
+    __builtin_amdgcn_raw_buffer_store_b32(w, r, static_cast<int>(off), 0, 0);
   } else {
     const uint32_t P0 = static_cast<uint32_t>(o[0]) | (static_cast<uint32_t>(o[1]) << 16);
     const uint32_t P1 = static_cast<uint32_t>(o[2]) | (static_cast<uint32_t>(o[3]) << 16);
@@ -160,11 +193,12 @@ __device__ __forceinline__ void store_strip(const GemmArgs &g, uint8_t *tile_out
     const uint32_t b1 = __builtin_amdgcn_mov_dpp(P1, 0x55, 0xF, 0xF, false);
     const uint32_t b2 = __builtin_amdgcn_mov_dpp(P1, 0xAA, 0xF, 0xF, false);
     const uint32_t b3 = __builtin_amdgcn_mov_dpp(P1, 0xFF, 0xF, 0xF, false);
-    const uint32_t sel = (q & 1) ? 0x07060302u : 0x05040100u;
-    const uint32_t lo_w = perm(a1, a0, sel), hi_w = perm(a3, a2, sel);
-    const uint32_t lo_w2 = perm(b1, b0, sel), hi_w2 = perm(b3, b2, sel);
-    const uint2 w = q < 2 ? make_uint2(lo_w, hi_w) : make_uint2(lo_w2, hi_w2);
-    if (ok) *reinterpret_cast<uint2 *>(tile_out + 2 * off) = w;
+    const uint32_t lo_w = perm(a1, a0, sl.sel), hi_w = perm(a3, a2, sl.sel);
+    const uint32_t lo_w2 = perm(b1, b0, sl.sel), hi_w2 = perm(b3, b2, sl.sel);
+    v2u w;
+    w.x = sl.upper ? lo_w2 : lo_w;
+    w.y = sl.upper ? hi_w2 : hi_w;
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, static_cast<int>(off), 0, 0);
   }
 }
 
@@ -475,8 +509,8 @@ __device__ __forceinline__ void k_tile(const MainCtx &c, int kt, int KT, uint8_t
 }
 
 // MODE 0: requantised output; MODE 1: exact int64 accumulators sum_k (a - zp) * w_int.
-// CLAMP: clamp t before rounding (some column cannot prove |t| < 2^30).
-template <bool A16, int MODE, bool CLAMP>
+// CLAMP: clamp t before rounding (some column cannot prove |t| < 2^30).  OUT16: 16-bit outputs.
+template <bool A16, int MODE, bool CLAMP, bool OUT16>
 __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArgs g) {
   using C = Cfg;
   // One LDS object per pipeline stage and operand: the compiler then knows that the
@@ -641,16 +675,26 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
   __syncthreads();
 #pragma unroll
   for (int b = 0; b < kBlocks; ++b) flagw[b * kGemmThreads + t] = 0u;  // this thread's own marks
-  const int esz = g.out16 ? 2 : 1;
-  uint8_t *const tile_out = static_cast<uint8_t *>(g.out) + (static_cast<size_t>(m0) * g.N + n0) * esz;
-  const bool full = m0 + rows_real <= M && n0 + cols_real <= g.N;
+  // Output addressing: one buffer resource over the tile's rows below M, and per lane the byte
+  // offset of its first store (row q of its quad's strip, 4 columns); a strip adds a
+  // compile-time row step times the row pitch.  A lane whose 32-column block lies past N (N is
+  // a multiple of 32) gets an offset past the resource, so its stores are dropped as well.
+  constexpr uint32_t esz = OUT16 ? 2u : 1u;
+  const uint32_t pitch = static_cast<uint32_t>(g.N) * esz;  // <= 2^21 bytes
+  const auto orsrc = out_rsrc(static_cast<uint8_t *>(g.out) + (static_cast<size_t>(m0) * g.N + n0) * esz,
+                              static_cast<uint32_t>(min(M - m0, rows_real)) * pitch);
+  const StripLane sl = strip_lane<OUT16>(q);
+  constexpr uint32_t kPast = 0x80000000u;  // > 128 rows x 2^21 bytes: past any tile's resource
   if (!A16) {
     static_for<kNT>([&](auto nt) {
       const int cl = wn * 64 + nt * 32 + (lane & 31);  // column inside the tile
       const double alpha = ctab[cl], beta = ctab[CB + cl], thr = ctab[2 * CB + cl];
+      const uint32_t off0 = n0 + wn * 64 + nt * 32 < g.N
+                                ? static_cast<uint32_t>(wm * 128 + 4 * (lane >> 5) + q) * pitch +
+                                      static_cast<uint32_t>(wn * 64 + nt * 32 + (lane & 28)) * esz
+                                : kPast;
       static_for<4>([&](auto mt) {
         static_for<4>([&](auto jg) {
-          const int R = wm * 128 + mt * 32 + 8 * jg + 4 * (lane >> 5);  // first of 4 rows
           int o[4];
           double dmax = 0.0;
           static_for<4>([&](auto jj) {
@@ -661,6 +705,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             o[jj] = clamp_out(oi, g.out_qmax);
           });
           if (dmax > thr) {  // rare: list the uncertain outputs of the strip with their sums
+            // the strip's first row, formed here: the common path does not need it
+            int rb = wm * 128 + 4 * (lane >> 5);
+            asm volatile("" : "+v"(rb));
+            const int R = rb + mt * 32 + 8 * jg;
             uint32_t keep = 0;
             static_for<4>([&](auto jjc) {
               constexpr int j = 4 * decltype(jg)::value + decltype(jjc)::value;
@@ -680,7 +728,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             });
             if (keep) flagb[((nt * 4 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(keep);
           }
-          store_strip(g, tile_out, m0, n0, R + q, wn * 64 + nt * 32 + (lane & 28), o, q, full);
+          store_strip<OUT16>(orsrc, off0 + row_step<mt * 32 + 8 * jg>(pitch), o, sl);
         });
       });
     });
@@ -692,9 +740,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
       constexpr int c = 0;  // one group of 32 real columns per wave
       const int cl = wn * 32 + (lane & 31);
       const double alpha = ctab[cl], alpha_m = ctab[CB + cl], beta = ctab[2 * CB + cl], thr = ctab[3 * CB + cl];
+      const uint32_t off0 = n0 + wn * 32 < g.N ? static_cast<uint32_t>(wm * 64 + 4 * (lane >> 5) + q) * pitch +
+                                                     static_cast<uint32_t>(wn * 32 + (lane & 28)) * esz
+                                               : kPast;
       static_for<2>([&](auto mt) {
         static_for<4>([&](auto jg) {
-          const int R = wm * 64 + mt * 32 + 8 * jg + 4 * (lane >> 5);
           auto t_of = [&](auto jj) {
             constexpr int j = 4 * decltype(jg)::value + decltype(jj)::value;
             const double X = fma(static_cast<double>(acc[2 * mt][2 * c][j]), 256.0, static_cast<double>(acc[2 * mt + 1][2 * c][j]));
@@ -710,6 +760,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             o[jj] = clamp_out(oi, g.out_qmax);
           });
           if (dmax > thr) {  // rare: list the uncertain outputs of the strip with their sums
+            // the strip's first row, formed here: the common path does not need it
+            int rb = wm * 64 + 4 * (lane >> 5);
+            asm volatile("" : "+v"(rb));
+            const int R = rb + mt * 32 + 8 * jg;
             uint32_t keep = 0;
             static_for<4>([&](auto jjc) {
               constexpr int j = 4 * decltype(jg)::value + decltype(jjc)::value;
@@ -729,7 +783,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
             });
             if (keep) flagb[((c * 2 + mt) * kGemmThreads + t) * 4 + jg] = static_cast<uint8_t>(keep);
           }
-          store_strip(g, tile_out, m0, n0, R + q, wn * 32 + (lane & 28), o, q, full);
+          store_strip<OUT16>(orsrc, off0 + row_step<mt * 32 + 8 * jg>(pitch), o, sl);
         });
       });
     }
@@ -852,7 +906,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
         fixup_one<A16>(g, m, n, lane);
       } else if (lane == 0) {
         const int oi = static_cast<int>(rd);
-        store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
+        store_out(g.out, OUT16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
       }
     }
     if (listed > kFixCap) {
@@ -977,7 +1031,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
               fixup_one<A16>(g, m, n, lane);
             } else if (lane == 0) {
               const int oi = static_cast<int>(rd);
-              store_out(g.out, g.out16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
+              store_out(g.out, OUT16, static_cast<size_t>(m) * g.N + n, oi < 0 ? 0 : (oi > g.out_qmax ? g.out_qmax : oi));
             }
           }
         }
@@ -992,10 +1046,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void qmm_gemm_kernel(const GemmArg
 template <bool A16, int MODE>
 qh_status launch(const GemmArgs &g, bool clamp, hipStream_t stream) {
   dim3 grid(g.TM * g.TN);
-  if (MODE == 0 && clamp)
-    hipLaunchKernelGGL((qmm_gemm_kernel<A16, MODE, true>), grid, dim3(kGemmThreads), 0, stream, g);
-  else
-    hipLaunchKernelGGL((qmm_gemm_kernel<A16, MODE, false>), grid, dim3(kGemmThreads), 0, stream, g);
+  if constexpr (MODE == 0) {
+    if (clamp && g.out16)
+      hipLaunchKernelGGL((qmm_gemm_kernel<A16, 0, true, true>), grid, dim3(kGemmThreads), 0, stream, g);
+    else if (clamp)
+      hipLaunchKernelGGL((qmm_gemm_kernel<A16, 0, true, false>), grid, dim3(kGemmThreads), 0, stream, g);
+    else if (g.out16)
+      hipLaunchKernelGGL((qmm_gemm_kernel<A16, 0, false, true>), grid, dim3(kGemmThreads), 0, stream, g);
+    else
+      hipLaunchKernelGGL((qmm_gemm_kernel<A16, 0, false, false>), grid, dim3(kGemmThreads), 0, stream, g);
+  } else {
+    hipLaunchKernelGGL((qmm_gemm_kernel<A16, MODE, false, false>), grid, dim3(kGemmThreads), 0, stream, g);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return hip_fail(err, "qmm_gemm_kernel launch");
   return QH_STATUS_OK;
