@@ -69,7 +69,6 @@ __device__ __forceinline__ long as_long(uint32_t lo, uint32_t hi) {
 // this rare path must not lower the occupancy of the stream.
 template <bool A16, int FMT, bool LPBQ, bool GA = false>
 __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, int lane) {
-  static_assert(!GA || !A16, "activations are read from global memory for 8-bit rows only");
   constexpr int WB = FMT == kTileI4 ? 16 : 32;
   const float sc = g.s32[n];
   const int KG = g.KG;
@@ -102,6 +101,7 @@ __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, 
       const int8_t *hp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(m) * g.ars + kg * 32);
       const int8_t *lp = reinterpret_cast<const int8_t *>(lds + static_cast<size_t>(g.M + m) * g.ars + kg * 32);
       const uint8_t *gp = g.act + static_cast<size_t>(m) * g.K + kg * 32;
+      const uint16_t *gp16 = reinterpret_cast<const uint16_t *>(g.act) + static_cast<size_t>(m) * g.K + kg * 32;
 #pragma unroll 4
       for (int j = 0; j < 32; ++j) {
         int w;
@@ -111,7 +111,8 @@ __device__ void gemv_fixup(const GemvArgs &g, const uint8_t *lds, int m, int n, 
         } else {
           w = static_cast<int8_t>((wd[u][j >> 2] >> (8 * (j & 3))) & 0xFFu);
         }
-        const int a = (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : (GA ? static_cast<int>(gp[j]) - 128 : static_cast<int>(hp[j]))) + off;
+        const int a = GA ? (A16 ? static_cast<int>(gp16[j]) : static_cast<int>(gp[j])) - g.act_zp
+                         : (A16 ? 256 * static_cast<int>(hp[j]) + lp[j] : static_cast<int>(hp[j])) + off;
         const float wf = static_cast<float>(w) * sc;
         s = fma(static_cast<double>(a) * g.sA, static_cast<double>(wf), s);
       }
@@ -370,12 +371,13 @@ constexpr int gemv_threads() {
   return MM == 16 && A16 ? 2 * kGemvThreads : kGemvThreads;
 }
 
-// RA (8-bit activations, 16 rows, K <= 16 kU k-groups): every lane keeps the A operands of its
-// slots in registers, loaded once from the activation matrix (the same for every group the
-// workgroup takes), instead of staging the rows in LDS.
+// RA (16 rows, K <= 16 kU k-groups; 16-bit activations with int4 codes): every lane keeps the A
+// operands of its slots in registers (16-bit activations: both byte planes), loaded once from the
+// activation matrix (the same for every group the workgroup takes), instead of staging the rows
+// in LDS.
 template <bool A16, int FMT, bool LPBQ, int MM, bool RA = false>
 __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2) : 4)) void qmm_gemv_kernel(const GemvArgs g) {
-  static_assert(!RA || (!A16 && MM == 16), "register-held activations: 8-bit activations, 16 rows");
+  static_assert(!RA || (MM == 16 && (!A16 || FMT == kTileI4)), "register-held activations: 16 rows");
   constexpr int NT = gemv_threads<A16, MM>();
   constexpr bool kWide = NT > kGemvThreads;
   constexpr int kUw = kWide ? kU / 2 : kU;  // slots of a batch per wave
@@ -480,29 +482,59 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
   // per thread and no registers to spare under their occupancy bound
   constexpr int kStageB = MM < 16 ? 1 : (A16 ? 4 : 8);
   int ustart = t + NT;  // the first unit of the staging loop below
-  uint4 areg[RA ? kU : 1][2];  // RA: activation row lane % 16, k-group of slot i (32 bytes)
+  // RA: activation row lane % 16, k-group of the wave's slot ii: 8-bit rows 32 bytes (a - 128);
+  // 16-bit rows the high-byte plane hi' = hi - 128 ([0], [1]) and the low-byte plane
+  // lo' = lo - 128 ([2], [3]), a - 32896 = 256 hi' + lo'
+  uint4 areg[RA ? kUw : 1][A16 ? 4 : 2];
   if constexpr (RA) {
     // the activation fragments first (L2: every workgroup reads the same rows), then the
     // per-group constants and the first group's weights (HBM)
     const int arow = min(lane & 15, M - 1);  // rows past M repeat row M - 1 (never stored)
 #pragma unroll
-    for (int i = 0; i < kU; ++i) {
-      const int kg = min(4 * (wave + 4 * i) + sub, KG - 1);
-      const uint4 *p = reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(arow) * g.K + kg * 32);
-      areg[i][0] = p[0];
-      areg[i][1] = p[1];
+    for (int ii = 0; ii < kUw; ++ii) {
+      const int kg = min(4 * (wave + 4 * (ii + shalf * kUw)) + sub, KG - 1);
+      if constexpr (A16) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(g.act) +
+                                                         static_cast<size_t>(arow) * g.K + kg * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) areg[ii][q] = p[q];
+      } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(g.act + static_cast<size_t>(arow) * g.K + kg * 32);
+        areg[ii][0] = p[0];
+        areg[ii][1] = p[1];
+      }
     }
+    if constexpr (HR) rtab_mant(blockIdx.x, rmt);
     load_epi(blockIdx.x);
     issue(blockIdx.x, 0);
     if (t < 16) r1[t] = 0;
     if (t == 0) fix_cnt = 0;
 #pragma unroll
-    for (int i = 0; i < kU; ++i)
+    for (int ii = 0; ii < kUw; ++ii) {
+      if constexpr (A16) {
+        // 8 u16 per uint4: XOR 0x80 on both bytes, then the high and the low bytes of k .. k + 31
+        uint32_t hv[8], lv[8];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        areg[i][q].x ^= 0x80808080u; areg[i][q].y ^= 0x80808080u;
-        areg[i][q].z ^= 0x80808080u; areg[i][q].w ^= 0x80808080u;
+        for (int q = 0; q < 4; ++q) {
+          uint4 v = areg[ii][q];
+          v.x ^= 0x80808080u; v.y ^= 0x80808080u; v.z ^= 0x80808080u; v.w ^= 0x80808080u;
+          hv[2 * q] = perm(v.y, v.x, 0x07050301u);
+          hv[2 * q + 1] = perm(v.w, v.z, 0x07050301u);
+          lv[2 * q] = perm(v.y, v.x, 0x06040200u);
+          lv[2 * q + 1] = perm(v.w, v.z, 0x06040200u);
+        }
+        areg[ii][0] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+        areg[ii][1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+        areg[ii][2] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+        areg[ii][3] = make_uint4(lv[4], lv[5], lv[6], lv[7]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          areg[ii][q].x ^= 0x80808080u; areg[ii][q].y ^= 0x80808080u;
+          areg[ii][q].z ^= 0x80808080u; areg[ii][q].w ^= 0x80808080u;
+        }
       }
+    }
     ustart = units;  // nothing to stage
   } else if constexpr (kLoop) {
     // 16 rows: the staged activations (L2) are requested first, then the per-group constants
@@ -624,8 +656,15 @@ __global__ __launch_bounds__((gemv_threads<A16, MM>()), (MM == 16 ? (A16 ? 1 : 2
               macc3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a.x, a.y), as_long(rr[2 * j], rr[2 * j + 1]), macc3, 0, 0, 0);
           }
           if (A16) {
-            const uint4 *lp4 = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(M + mrow) * g.ars + kg * 32);
-            const uint4 al0 = lp4[0], al1 = lp4[1];
+            uint4 al0, al1;
+            if constexpr (RA) {
+              al0 = areg[ii][A16 ? 2 : 0];
+              al1 = areg[ii][A16 ? 3 : 1];
+            } else {
+              const uint4 *lp4 = reinterpret_cast<const uint4 *>(lds + static_cast<size_t>(M + mrow) * g.ars + kg * 32);
+              al0 = lp4[0];
+              al1 = lp4[1];
+            }
             const uint2 al[4] = {make_uint2(al0.x, al0.y), make_uint2(al0.z, al0.w), make_uint2(al1.x, al1.y), make_uint2(al1.z, al1.w)};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -913,8 +952,9 @@ qh_status launch_mm(const GemvArgs &g, size_t dyn_lds, hipStream_t stream) {
   const int groups = g.N / 16;
   if (g.M <= 1) return launch_one<A16, FMT, LPBQ, 1>(g, dim3(groups), dyn_lds, stream);
   if (g.M <= 4) return launch_one<A16, FMT, LPBQ, 4>(g, dim3(groups), dyn_lds, stream);
-  // 8-bit rows whose k-groups fit one batch per lane (K <= 16 kU x 32) stay in registers
-  if constexpr (!A16)
+  // rows whose k-groups fit one batch per lane (K <= 16 kU x 32) stay in registers (8-bit
+  // activations, and 16-bit activations with int4 codes)
+  if constexpr (!A16 || FMT == kTileI4)
     if (g.KG <= 16 * kU) return launch_16<A16, FMT, LPBQ, true>(g, 0, stream);
   return launch_16<A16, FMT, LPBQ, false>(g, dyn_lds, stream);
 }
