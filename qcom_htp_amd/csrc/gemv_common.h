@@ -18,11 +18,19 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
 // int8 weight bytes of 4 int4 codes: nibbles u (offset-binary, code = u - 8) times the LPBQ block
 // scale f, as (u * f + 128 - 8 f) ^ 0x80 per byte.  u * f <= 240 and 128 - 8 f >= 0 keep every
 // byte of the product and the sum below 256 (no carries between bytes); f = 0 gives zero weights.
+// The multiply-add runs on the two 16-bit halves (one packed v_pk_mad_u16 at the full rate; a
+// 32-bit integer multiply issues at a quarter of it): each half holds two bytes, and no byte
+// carries, so no half overflows.
 __device__ __forceinline__ uint32_t w4_to_i8(uint32_t u4, uint32_t f) {
-  return (u4 * f + (128u - 8u * f) * 0x01010101u) ^ 0x80808080u;
+  const unsigned short fs = static_cast<unsigned short>(f);
+  const unsigned short cs = static_cast<unsigned short>((128u - 8u * f) * 0x0101u);
+  const us2 r = __builtin_bit_cast(us2, u4) * us2{fs, fs} + us2{cs, cs};
+  return __builtin_bit_cast(uint32_t, r) ^ 0x80808080u;
 }
 
 // 16-bit activations, int4 codes: the float32 rounding residue r = fl32(w s32) / 2^E - w M of a
