@@ -1,39 +1,29 @@
-// GDN / KDA per-head triangular solve T = (I - A)^-1, A strictly lower triangular, C <= 256, by
-// recursive doubling with matrix-core merges.
+// GDN / KDA per-head triangular solve T = (I - A)^-1, A strictly lower triangular, C <= 256
+// (C % 16 == 0, NB = C / 16 diagonal blocks), by block forward substitution over 16-column
+// strips on the matrix cores.
 //
-// C is padded to P = 2^p >= C (zero A there, so the padding's T is the identity and never
-// couples to the rest):
 //   level 0: the 16 x 16 diagonal blocks T_bb = (I - A_bb)^-1 by forward substitution in fp32,
 //            one lane per column;
-//   level s = 16, 32, .., P/2: pairs of diagonal blocks of size s merge into blocks of size 2s,
-//            [T11 0; A21 T22] -> [T11 0; T21 T22] with T21 = T22 (A21 T11)
-//            -- the block-recursive merge of GdnSolveBR (M = A21 T11, T21 = T22 M,
-//            example/gdn_native/solve_br_op/src/gdn_solve_br_core.h:1-8) applied at every
-//            level, which equals the block merges T_ij = T_ii sum_k A_ik T_kj of
-//            example/gdn_native/solve_op/src/gdn_solve_core.h:50-72: log2(P / 16) dependent
-//            levels instead of P / 16 - 1 block steps.
-// Work split: G = P / 32 workgroups (8 waves each) per head.  Every workgroup of a head computes
-// the two block-diagonal halves (levels 0 .. P/4) itself -- short, latency-bound levels whose
-// redundancy costs less than a cross-workgroup exchange -- then one 16-column strip of the last
-// merge (T21 rows P/2 .. P-1).  The G workgroups of a head get block indexes of one residue mod
-// 8, which places them on one XCD and one L2.
-// Inside the halves a level gives each wave one 16-row tile of one merge's T21:
-//   Y[i][:] = A21[i][:] T11, written to LDS transposed in the merge's upper-right block (the
-//            zero block T12, which no product ever reads), then
-//   X[i][:] = sum_{l <= i} T22[i][l] Y[l][:]  (registers; into the T21 region at once).
+//   strip j: X = T[:, 16 j .. 16 j + 15] solves (I - A) X = E_j, block by block:
+//            X_j = T_jj,  X_b = T_bb sum_{j <= c < b} A_bc X_c  (b = j + 1 .. NB - 1),
+//            the block merges T_ij = T_ii sum_k A_ik T_kj of
+//            example/gdn_native/solve_op/src/gdn_solve_core.h:50-72 taken one column strip at
+//            a time.
+// One wave runs one strip.  Its X_c stay in registers in the MFMA result layout, which is also
+// the B operand layout of the next products (bf16_split.h), so the NB - 1 - j steps of a strip
+// need no barrier and no LDS round trip for X; the A blocks and T_bb are LDS reads, issued one
+// step ahead.  Every strip reads A's strictly lower blocks, so a workgroup stages them in LDS
+// once, as ready operand records.
+// Work split: G = 2 workgroups (8 waves) per head for NB > 8, one otherwise.  Strips k and
+// NB - 1 - k share a SIMD (waves w and w + 4), so the longest strip (k = 0) has its SIMD's matrix
+// core nearly to itself.  The G workgroups of a head get block indexes of one residue mod 8,
+// which places them on one XCD and one L2.
 // The products run on v_mfma_f32_16x16x32_bf16: a 32-deep k step takes rows 4q .. 4q+3 of two
 // 16-row blocks, the k order in which the MFMA result layout (lane: rows 4q .. 4q+3 of one
 // column) is read back as the next B operand.
-// LDS holds T's block-diagonal halves (row r holds the columns of its half) as packed bf16
-// hi | lo words (lo = bf16(x - hi)), the form the MFMA operands take; each level's fp32 results
-// go to global memory from registers, so T is exact fp32 accumulation output.
-// Memory order: one counter tracks vector loads and stores together, so a wait for a load also
-// waits for every store issued before it.  All of a workgroup's A reads are therefore issued at
-// the start, straight-line (a skipped read becomes a discarded read), level 0's first; stores
-// only follow.
 // Precision: QH_GDN_FP32 multiplies hi/lo splits (hi*hi + hi*lo + lo*hi, fp32 accumulation:
 // about 16 significant bits per product); QH_GDN_BF16 multiplies the hi parts only.  The
-// diagonal blocks are fp32 in both.
+// diagonal blocks are fp32 in both, and T is stored from the fp32 accumulators.
 // The u16 variant applies the GdnSolve op's code contract on load / store
 // (A = (code - zpA) * sA; T_code = clip(rint(T / sT) + zpT, 0, 65535)).
 
@@ -45,15 +35,17 @@ namespace {
 
 using namespace bf16s;
 
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
 constexpr int kRdThreads = 512;
-constexpr int kTs = 132;   // LDS row stride of the T store, words (conflict-free column reads)
 constexpr int kAtRow = 20;  // staged diagonal block A^T: row stride (16-byte aligned rows) ..
 constexpr int kAtBlk = 336;  // .. and block stride (= 16 mod 64 banks: the 4 blocks of a wave differ)
 
 struct GdnArgs {
   const void *A;
   void *T;
-  int C, P, half, groups, heads;
+  int C, groups, heads;
   int zpA, zpT;
   float sA, sT, inv_sT;
 };
@@ -90,124 +82,46 @@ __device__ __forceinline__ uint16_t t_code(const GdnArgs &g, float v) {
   return static_cast<uint16_t>(q);
 }
 
-template <bool U16>
-__device__ __forceinline__ void store_t(const GdnArgs &g, size_t idx, float v) {
-  if (U16) {
-    static_cast<uint16_t *>(g.T)[idx] = t_code<U16>(g, v);
-  } else {
-    static_cast<float *>(g.T)[idx] = v;
-  }
+// Stages a diagonal-block row quarter (row i, columns 4 k4 .. + 3 of block bb) transposed.
+__device__ __forceinline__ void stage_at(float *dstage, int bb, int i, int k4, const float4 v) {
+  float *d = dstage + bb * kAtBlk + (4 * k4) * kAtRow + i;
+  d[0] = v.x;
+  d[kAtRow] = v.y;
+  d[2 * kAtRow] = v.z;
+  d[3 * kAtRow] = v.w;
 }
 
-// The MFMA result tile acc (rows row0 + 4q + e, column col) to T.
-template <bool U16>
-__device__ __forceinline__ void store_tile(const GdnArgs &g, size_t hbase, int row0, int col, int q, const v4f &acc) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) store_t<U16>(g, hbase + static_cast<size_t>(row0 + 4 * q + e) * g.C + col, acc[e]);
+constexpr int kFsMaxNB = 16;
+constexpr int kFsLowBlocks = kFsMaxNB * (kFsMaxNB - 1) / 2;  // strictly lower 16 x 16 blocks
+constexpr int kFsTd = 16;  // Td row stride, words
+
+// Word column of column c in row r of a 16 x 16 LDS block: the 4-word quarters of row r are
+// XOR-swizzled by r / 4.  An A operand read (lane: row r16, quarter q, 16 bytes) then puts the 16
+// lanes of a quarter on 16 distinct 16-byte bank groups; unswizzled, rows 64 bytes apart shared 4
+// groups (4-way bank conflicts on every read).
+__device__ __forceinline__ int fs_col(int r, int c) { return ((((c >> 2) ^ (r >> 2)) & 3) << 2) | (c & 3); }
+
+// Strip of wave `wave` in workgroup `part`: pair k = 4 part + wave % 4, strip k for waves 0..3 and
+// NB - 1 - k for waves 4..7 (none when that would repeat strip k or lie past NB).
+__device__ __forceinline__ int fs_strip(int NB, int part, int wave) {
+  const int k = 4 * part + (wave & 3);
+  const int j = wave < 4 ? k : NB - 1 - k;
+  return (j < NB && (wave < 4 || j > k)) ? j : -1;
 }
 
-// Wave -> (merge at row b, tile i) of a level inside the halves (NB tiles per block): P / 32
-// tasks, one per wave.  Waves w and w + 4 share a SIMD; the T22 product of tile i costs i + 1 k
-// blocks, so the second half of the waves takes the tiles of its merge in reverse order.
-template <int NB>
-__device__ __forceinline__ void tile_task(int wave, int &b, int &i) {
-  const int m = wave / NB, ii = wave % NB;
-  i = wave >= 4 ? NB - 1 - ii : ii;
-  b = 32 * NB * m;
-}
-
-// A21 row blocks of tile i of the merge at row b (NB = s / 16): block l holds row b + s + 16 i +
-// r16, columns b + 16 l + 4q .. + 3 (zero past C or when !ok).
-template <bool U16, int NB>
-__device__ __forceinline__ void load_tile(const GdnArgs &g, size_t hbase, int b, int i, bool ok, int lane,
-                                          float4 (&av)[NB]) {
-  constexpr int s = 16 * NB;
-  const int r16 = lane & 15, q = lane >> 4;
-#pragma unroll
-  for (int l = 0; l < NB; ++l)
-    av[l] = load_a4_or0<U16>(g, hbase, b + s + 16 * i + r16, b + 16 * l + 4 * q,
-                             ok && b + s + 16 * i < g.C && b + 16 * l < g.C);
-}
-
-// One merge level inside the halves (NB tiles per block), tile i of the merge at row b per task
-// wave; `owner` marks the workgroup that stores this task's T21 tile.  Two barriers: Y complete
-// (in the upper-right block, rows b .. b + s, columns b + s .. b + 2 s), then X complete (in the
-// T21 region, which no wave reads during the X products).
-template <bool U16, bool SPLIT, int NB>
-__device__ __forceinline__ void merge_level(const GdnArgs &g, size_t hbase, uint32_t (*Tl)[kTs], bool task, bool owner,
-                                            int b, int i, const float4 (&av)[NB], int lane) {
-  constexpr int s = 16 * NB;
-  const int r16 = lane & 15, q = lane >> 4;
-  const int shift = b >= g.half ? g.half : 0;  // Tl column offset of this merge's rows
-  const int rt = b + s + 16 * i;                // first row of this wave's tile
-  if (task) {
-    Half4 as[NB];
-#pragma unroll
-    for (int l = 0; l < NB; ++l) as[l] = split4<SPLIT>(av[l]);
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {  // strip j: T11 is zero above block j, so k blocks l = j ..
-      const int c = b - shift + 16 * j + r16;
-      v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int l = j; l < NB; l += 2) {
-        const bool two = l + 1 < NB;
-        const int r0 = b + 16 * l + 4 * q;
-        const Half4 t0 = unpack4(Tl[r0][c], Tl[r0 + 1][c], Tl[r0 + 2][c], Tl[r0 + 3][c]);
-        const Half4 t1 = two ? unpack4(Tl[r0 + 16][c], Tl[r0 + 17][c], Tl[r0 + 18][c], Tl[r0 + 19][c]) : kZero4;
-        acc = mma<SPLIT>(as[l], two ? as[l + 1] : kZero4, t0, t1, acc);
-      }
-      // Y tile (i, j) transposed at tile (i, j) of the upper-right block: row b + 16 i + column,
-      // column b + s + 16 j + row (half-local)
-      *reinterpret_cast<uint4 *>(&Tl[b + 16 * i + r16][b - shift + s + 16 * j + 4 * q]) =
-          make_uint4(hilo<SPLIT>(acc[0]), hilo<SPLIT>(acc[1]), hilo<SPLIT>(acc[2]), hilo<SPLIT>(acc[3]));
-    }
-  }
-  lds_barrier();
-  v4f X[NB];
-#pragma unroll
-  for (int j = 0; j < NB; ++j) X[j] = v4f{0.f, 0.f, 0.f, 0.f};
-  if (task) {
-    const uint32_t *trow = Tl[rt + r16];
-    for (int l = 0; l <= i; l += 2) {  // wave-uniform bounds
-      const bool two = l + 1 <= i;
-      const int cA = b + s - shift + 16 * l + 4 * q;  // Tl column of T22's block l, this lane's k
-      const Half4 w0 = unpack4(*reinterpret_cast<const uint4 *>(trow + cA));
-      const Half4 w1 = two ? unpack4(*reinterpret_cast<const uint4 *>(trow + cA + 16)) : kZero4;
-      const uint32_t *yrow = Tl[b + 16 * l + r16];  // transposed Y tile (l, j): column r16 of it
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int c = b - shift + s + 16 * j + 4 * q;
-        const Half4 y0 = unpack4(*reinterpret_cast<const uint4 *>(yrow + c));
-        const Half4 y1 = two ? unpack4(*reinterpret_cast<const uint4 *>(yrow + 16 * kTs + c)) : kZero4;
-        X[j] = mma<SPLIT>(w0, w1, y0, y1, X[j]);
-      }
-    }
-    if (owner && rt < g.C) {
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-        if (b + 16 * j < g.C) store_tile<U16>(g, hbase, rt, b + 16 * j + r16, q, X[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) Tl[rt + 4 * q + e][b - shift + 16 * j + r16] = hilo<SPLIT>(X[j][e]);
-    }
-  }
-  lds_barrier();
-}
-
-// Level 0 from the staged, transposed diagonal blocks (At[k][r] = A[r][k]): block t / 16, column
-// jc = t % 16 per thread, by a column sweep -- at step i, x_i is final and every later row takes
-// A[r][i] x_i -- which keeps each x_r's sum in the order k = 0, 1, .. of plain forward
-// substitution while the dependent chain is one FMA per step.  Results into LDS; the workgroup
-// `part` stores blocks 2 part and 2 part + 1.
-template <bool U16, bool SPLIT>
-__device__ __forceinline__ void level0(const GdnArgs &g, size_t hbase, uint32_t (*Tl)[kTs], const float *dstage,
-                                       int nblocks, int part, int t) {
+// Level 0 into Td (T_bb as hi | lo words, row-major with fs_col quarters) from the staged
+// transposed diagonal blocks (At[k][r] = A[r][k]): block t / 16, column jc = t % 16 per thread, by
+// a column sweep -- at step i, x_i is final and every later row takes A[r][i] x_i -- which keeps
+// each x_r's sum in the order k = 0, 1, .. of plain forward substitution while the dependent
+// chain is one FMA per step.  T_bb also goes, in fp32 and row-major, over its own staged block
+// in dstage (read only by this wave, and fully read by the time the sweep ends), for the wave of
+// strip bb to store: stores issued here kept the strips waiting (their data registers are reused
+// by the strips, and the compiler then waits for the stores).
+template <bool SPLIT>
+__device__ __forceinline__ void fs_level0(uint32_t (*Td)[16][kFsTd], float *dstage, int NB, int t) {
   const int bb = t >> 4, jc = t & 15;
-  if (bb < nblocks) {
-    // column i of A (rows 0 .. 15) = row i of At: 4 aligned float4, two columns read ahead
-    const float4 *At = static_cast<const float4 *>(__builtin_assume_aligned(dstage + bb * kAtBlk, 16));
+  if (bb < NB) {
+    const float4 *At = static_cast<const float4 *>(__builtin_assume_aligned(dstage + bb * kAtBlk, 16));  // A_bb^T
     float x[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] = (r == jc) ? 1.0f : 0.0f;
@@ -234,207 +148,251 @@ __device__ __forceinline__ void level0(const GdnArgs &g, size_t hbase, uint32_t 
           if (4 * m + e > i) x[4 * m + e] = fmaf(vv[e], xi, x[4 * m + e]);
       }
     }
-    const int col0 = 16 * bb + jc;
-    const int lcol = col0 - (16 * bb >= g.half ? g.half : 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) Tl[16 * bb + i][lcol] = hilo<SPLIT>(x[i]);
-    if ((bb >> 1) == part && 16 * bb < g.C) {
+    for (int i = 0; i < 16; ++i) Td[bb][i][fs_col(i, jc)] = hilo<SPLIT>(x[i]);
+    float *const tf = dstage + bb * kAtBlk;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) store_t<U16>(g, hbase + static_cast<size_t>(16 * bb + i) * g.C + col0, x[i]);
-    }
+    for (int i = 0; i < 16; ++i) tf[16 * i + jc] = x[i];
   }
 }
 
-// Stages a diagonal-block row quarter (row i, columns 4 k4 .. + 3 of block bb) transposed.
-__device__ __forceinline__ void stage_at(float *dstage, int bb, int i, int k4, const float4 v) {
-  float *d = dstage + bb * kAtBlk + (4 * k4) * kAtRow + i;
-  d[0] = v.x;
-  d[kAtRow] = v.y;
-  d[2 * kAtRow] = v.z;
-  d[3 * kAtRow] = v.w;
-}
-
-// Zeros above the block diagonal: workgroup `part` of `groups` takes rows part, part + groups, ..,
-// one row per wave at a time, one float4 per lane (C / 4 <= 64).
+// The MFMA result tile acc (lane: rows row0 + 4q + e of column col0 + r16) to T by rows: the 4
+// lanes of a quad transpose their 4 x 4 values in two DPP butterfly stages (partner lane p ^ 1,
+// then p ^ 2), after which lane 4a + p holds row row0 + 4q + p, columns col0 + 4a .. + 3 and
+// stores them at once (one 16-byte store where the column layout took four 4-byte ones).  The
+// store is a buffer store: the tile's offset (row0 C + col0 elements) is a scalar and the lane's
+// part (lane_off) one register for the whole strip, so no per-store address register is
+// rewritten while earlier stores may still read theirs.
 template <bool U16>
-__device__ __forceinline__ void store_zeros(const GdnArgs &g, size_t hbase, int part, int wave, int lane) {
-  const int C = g.C;
-  for (int row = part + wave * g.groups; row < C; row += 8 * g.groups) {
-    const int c = 4 * lane;
-    if (c < C && c >= 16 * (row / 16) + 16) {
-      const size_t idx = hbase + static_cast<size_t>(row) * C + c;
-      if (U16) {
-        const uint32_t z = static_cast<uint32_t>(g.zpT) * 0x10001u;  // code of 0.0: clip(zpT)
-        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(g.T) + idx) = make_uint2(z, z);
-      } else {
-        *reinterpret_cast<float4 *>(static_cast<float *>(g.T) + idx) = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+__device__ __forceinline__ void store_tile_rows(const GdnArgs &g, __amdgpu_buffer_rsrc_t tr, uint32_t lane_off,
+                                                int row0, int col0, int lane, const v4f &acc, float (&w)[4]) {
+  const int p = lane & 3;
+  float u[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[e ^ 1]), 0xB1, 0xF, 0xF, false));
+    u[e] = ((e ^ p) & 1) ? o : acc[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(u[e ^ 2]), 0x4E, 0xF, 0xF, false));
+    w[e] = ((e ^ p) & 2) ? o : u[e];
+  }
+  const int soff = __builtin_amdgcn_readfirstlane((row0 * g.C + col0) * (U16 ? 2 : 4));
+  if (U16) {
+    const uint32_t c01 = t_code<U16>(g, w[0]) | (static_cast<uint32_t>(t_code<U16>(g, w[1])) << 16);
+    const uint32_t c23 = t_code<U16>(g, w[2]) | (static_cast<uint32_t>(t_code<U16>(g, w[3])) << 16);
+    __builtin_amdgcn_raw_buffer_store_b64(v2u{c01, c23}, tr, static_cast<int>(lane_off), soff, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]), __float_as_uint(w[3])},
+                                           tr, static_cast<int>(lane_off), soff, 0);
   }
 }
 
-// The solve for padded size P = 2^LOGP (32 <= P <= 256) by workgroup `part` of G = P / 32.
-template <bool U16, bool SPLIT, int LOGP>
-__device__ __forceinline__ void solve_head(const GdnArgs &g, uint32_t (*Tl)[kTs], float *dstage, int part,
-                                           size_t hbase, int t, int wave, int lane) {
-  constexpr int P = 1 << LOGP;
-  constexpr int NBF = P / 32;  // 16-row tiles per block of the last merge
-  const int C = g.C;
+// One wave's strip j (after level 0, with Al, Td and the fp32 T_bb in dstage staged): T_jj, then
+// the strip's steps, each tile stored as it is computed.
+template <bool U16, bool SPLIT>
+__device__ __forceinline__ void fs_strip_solve(const GdnArgs &g, size_t hbase, const uint32_t (*Al)[16][16],
+                                               const uint32_t (*Td)[16][kFsTd], const float *dstage, int NB, int j,
+                                               int lane) {
   const int r16 = lane & 15, q = lane >> 4;
-  // ---- A reads: level 0's, then each level's, straight-line ---------------------------------------
-  float4 dv[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {  // float4 slot t + 512 u: block wave + 8 u, row (t / 4) % 16, quarter t % 4
-    const int bb = wave + 8 * u, i = (lane >> 2) & 15, k4 = lane & 3;
-    dv[u] = load_a4_or0<U16>(g, hbase, 16 * bb + i, 16 * bb + 4 * k4, bb < P / 16 && 16 * bb < C);
+  // Blocks are indexed relative to the strip (u = c - j, v = b - j), so every step's loops have
+  // compile-time bounds: a step is one basic block whose LDS reads all issue before its products
+  // (guards per block pair made each pair wait for its own reads).
+  Half4 xs[kFsMaxNB];  // X_{j+u} as B operands (rows 4q .. 4q + 3 of column r16)
+  // The stored values of every step stay allocated until the strip ends: when a later step's LDS
+  // reads reused a store's data registers, the compiler made them wait for the whole store.
+  float wk[kFsMaxNB][4];
+  // T of this head as a buffer (C x C elements) and this lane's offset in a stored tile: row
+  // 4q + p, columns 4a .. 4a + 3 (lane 16 q + 4 a + p)
+  const size_t esz = U16 ? 2 : 4;
+  const __amdgpu_buffer_rsrc_t tr = __builtin_amdgcn_make_buffer_rsrc(
+      static_cast<uint8_t *>(g.T) + hbase * esz, 0, static_cast<int>(static_cast<size_t>(g.C) * g.C * esz), 0x00020000);
+  const uint32_t lane_off = static_cast<uint32_t>(((4 * q + (lane & 3)) * g.C + (r16 & 12)) * esz);
+  {
+    const float *tf = dstage + j * kAtBlk;  // T_jj in fp32, row-major
+    const v4f xj = {tf[16 * (4 * q) + r16], tf[16 * (4 * q + 1) + r16], tf[16 * (4 * q + 2) + r16], tf[16 * (4 * q + 3) + r16]};
+    store_tile_rows<U16>(g, tr, lane_off, 16 * j, 16 * j, lane, xj, wk[0]);
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep level 0's reads first: its wait then covers only them
-  const bool task = wave < P / 32;
-  const bool owner = wave == part;  // this workgroup stores task `part` of every level
-  int b1 = 0, i1 = 0, b2 = 0, i2 = 0, b4 = 0, i4 = 0;
-  float4 a1[1], a2[2], a4[4];
-  if (P > 32) {
-    tile_task<1>(wave, b1, i1);
-    load_tile<U16, 1>(g, hbase, b1, i1, task, lane, a1);
+  xs[0] = unpack4(Td[j][4 * q][fs_col(4 * q, r16)], Td[j][4 * q + 1][fs_col(4 * q + 1, r16)],
+                  Td[j][4 * q + 2][fs_col(4 * q + 2, r16)], Td[j][4 * q + 3][fs_col(4 * q + 3, r16)]);
+  const int steps = NB - 1 - j;
+  const int qs = fs_col(r16, 4 * q);  // this lane's quarter in its row of a block
+  // A step's operands (the operand records of its A blocks and its T_bb) are read during the step
+  // before: the reads of a step issued at its start left one LDS round trip per few products on
+  // the strip's critical path.  Reads for a step past the last one fetch block 0 (never used).
+  uint4 rc[kFsMaxNB];
+  uint4 tc;
+  {
+    const bool any = steps > 0;
+    rc[0] = *reinterpret_cast<const uint4 *>(&Al[any ? (j + 1) * j / 2 + j : 0][r16][qs]);
+    tc = *reinterpret_cast<const uint4 *>(&Td[any ? j + 1 : 0][r16][qs]);
   }
-  if (P > 64) tile_task<2>(wave, b2, i2);
-  if (P > 128) tile_task<4>(wave, b4, i4);
-  // last merge, strip `part`, tile `wave`: k blocks l = part + 2 p + h
-  constexpr int kPF = (NBF + 1) / 2;
-  float4 af[kPF][2];
-  auto load_last = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < kPF; ++p) {
+  for (int v = 1; v < kFsMaxNB; ++v) {
+    if (v > steps) continue;  // uniform (a break would stop the unrolling)
+    const int b = j + v;
+    const bool more = v < steps;
+    const int nbase = more ? (b + 1) * b / 2 + j : 0;  // the next step's row of A blocks
+    const int nstep = more ? 1 : 0;
+    uint4 rn[kFsMaxNB];
+    // Y = sum_{u < v} A_{b, j+u} X_{j+u} over pairs (u, u + 1); products go to kAcc accumulators
+    // in turn (with SPLIT one per product kind), so consecutive products do not wait for each other
+    constexpr int kAcc = SPLIT ? 3 : 2;
+    v4f acc[kAcc];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int l = part + 2 * p + h;
-        af[p][h] = load_a4_or0<U16>(g, hbase, P / 2 + 16 * wave + r16, 16 * l + 4 * q,
-                                    wave < NBF && l < NBF && P / 2 + 16 * wave < C && 16 * l < C);
+    for (int i = 0; i < kAcc; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < v; u += 2) {
+      const Half4 a0 = {rc[u].x, rc[u].y, rc[u].z, rc[u].w};
+      const Half4 a1 = u + 1 < v ? Half4{rc[u + 1].x, rc[u + 1].y, rc[u + 1].z, rc[u + 1].w} : kZero4;
+      rn[u] = *reinterpret_cast<const uint4 *>(&Al[nbase + nstep * u][r16][qs]);
+      rn[u + 1] = *reinterpret_cast<const uint4 *>(&Al[nbase + nstep * (u + 1)][r16][qs]);
+      const Half4 &b0 = xs[u], &b1 = u + 1 < v ? xs[u + 1] : kZero4;
+      constexpr int kPer = SPLIT ? 3 : 1;
+      const int s0 = (u / 2) * kPer;  // compile-time: the loop is unrolled
+      acc[s0 % kAcc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_hi(a0, a1), op_hi(b0, b1), acc[s0 % kAcc], 0, 0, 0);
+      if (SPLIT) {
+        acc[(s0 + 1) % kAcc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_hi(a0, a1), op_lo(b0, b1), acc[(s0 + 1) % kAcc], 0, 0, 0);
+        acc[(s0 + 2) % kAcc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_lo(a0, a1), op_hi(b0, b1), acc[(s0 + 2) % kAcc], 0, 0, 0);
       }
     }
-  };
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- level 0 ------------------------------------------------------------------------------------
+    if ((v & 1) == 0) rn[v] = *reinterpret_cast<const uint4 *>(&Al[nbase + nstep * v][r16][qs]);
+    v4f y = acc[0];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int bb = wave + 8 * u, i = (lane >> 2) & 15, k4 = lane & 3;
-    if (bb < P / 16) stage_at(dstage, bb, i, k4, dv[u]);
-  }
-  lds_barrier();
-  level0<U16, SPLIT>(g, hbase, Tl, dstage, P / 16, part, t);
-  lds_barrier();
-  store_zeros<U16>(g, hbase, part, wave, lane);
-
-  // ---- merges inside the halves -------------------------------------------------------------------
-  // Each level's A tiles are requested one level ahead (the last merge's strip two ahead), so the
-  // requests are issued a few at a time; the stores issued before them are a level old by the
-  // time the wait for them (which counts those stores too) comes.
-  if (P > 64) load_tile<U16, 2>(g, hbase, b2, i2, task, lane, a2);
-  if (P <= 128) load_last();
-  if (P > 32) merge_level<U16, SPLIT, 1>(g, hbase, Tl, task, owner, b1, i1, a1, lane);
-  if (P > 128) load_tile<U16, 4>(g, hbase, b4, i4, task, lane, a4);
-  if (P > 64) merge_level<U16, SPLIT, 2>(g, hbase, Tl, task, owner, b2, i2, a2, lane);
-  if (P > 128) load_last();
-  if (P > 128) merge_level<U16, SPLIT, 4>(g, hbase, Tl, task, owner, b4, i4, a4, lane);
-
-  // ---- last merge, strip `part`: Y tiles (one per wave) through LDS, then T21 = T22 Y -----------
-  // Y tiles, transposed (ybuf[tile][column][row]): level 0 is done with the staging area
-  uint32_t(*ybuf)[16][16] = reinterpret_cast<uint32_t(*)[16][16]>(dstage);
-  if (wave < NBF) {
-    v4f y = {0.f, 0.f, 0.f, 0.f};
-    const int c = 16 * part + r16;  // T11 is in the first half: Tl column = T column
+    for (int i = 1; i < kAcc; ++i) y += acc[i];
+    // X_b = T_bb Y: T_bb as the A operand (row r16, columns 4q .. 4q + 3), Y as the B operand;
+    // the split products into separate accumulators as well
+    const Half4 tb = unpack4(tc);
+    tc = *reinterpret_cast<const uint4 *>(&Td[more ? b + 1 : 0][r16][qs]);
+    const Half4 ys = split4<SPLIT>(y);
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+    v4f x = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_hi(tb, kZero4), op_hi(ys, kZero4), z, 0, 0, 0);
+    if (SPLIT) {
+      const v4f x1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_hi(tb, kZero4), op_lo(ys, kZero4), z, 0, 0, 0);
+      const v4f x2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(op_lo(tb, kZero4), op_hi(ys, kZero4), z, 0, 0, 0);
+      x += x1 + x2;
+    }
+    store_tile_rows<U16>(g, tr, lane_off, 16 * b, 16 * j, lane, x, wk[v]);
+    xs[v] = split4<SPLIT>(x);
 #pragma unroll
-    for (int p = 0; p < kPF; ++p) {
-      const int l = part + 2 * p;
-      if (l >= NBF) break;  // part is uniform: a scalar branch
-      const bool two = l + 1 < NBF;
-      const int r0 = 16 * l + 4 * q;
-      const Half4 t0 = unpack4(Tl[r0][c], Tl[r0 + 1][c], Tl[r0 + 2][c], Tl[r0 + 3][c]);
-      const Half4 t1 = two ? unpack4(Tl[r0 + 16][c], Tl[r0 + 17][c], Tl[r0 + 18][c], Tl[r0 + 19][c]) : kZero4;
-      y = mma<SPLIT>(split4<SPLIT>(af[p][0]), two ? split4<SPLIT>(af[p][1]) : kZero4, t0, t1, y);
-    }
-    *reinterpret_cast<uint4 *>(&ybuf[wave][r16][4 * q]) =
-        make_uint4(hilo<SPLIT>(y[0]), hilo<SPLIT>(y[1]), hilo<SPLIT>(y[2]), hilo<SPLIT>(y[3]));
+    for (int u = 0; u <= v; ++u) rc[u] = rn[u];
   }
-  lds_barrier();
-  if (wave < NBF) {
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    const uint32_t *trow = Tl[P / 2 + 16 * wave + r16];  // T22 row; its Tl columns start at 0
-    for (int l = 0; l <= wave; l += 2) {  // wave-uniform bounds
-      const bool two = l + 1 <= wave;
-      const Half4 w0 = unpack4(*reinterpret_cast<const uint4 *>(trow + 16 * l + 4 * q));
-      const Half4 w1 = two ? unpack4(*reinterpret_cast<const uint4 *>(trow + 16 * l + 16 + 4 * q)) : kZero4;
-      const Half4 y0 = unpack4(*reinterpret_cast<const uint4 *>(&ybuf[l][r16][4 * q]));
-      const Half4 y1 = two ? unpack4(*reinterpret_cast<const uint4 *>(&ybuf[l + 1][r16][4 * q])) : kZero4;
-      acc = mma<SPLIT>(w0, w1, y0, y1, acc);
-    }
-    if (P / 2 + 16 * wave < C && 16 * part < C) store_tile<U16>(g, hbase, P / 2 + 16 * wave, 16 * part + r16, q, acc);
-  }
+#pragma unroll
+  for (int v = 0; v < kFsMaxNB; ++v)
+    if (v <= steps) asm volatile("" ::"v"(wk[v][0]), "v"(wk[v][1]), "v"(wk[v][2]), "v"(wk[v][3]));
 }
 
 template <bool U16, bool SPLIT>
-__global__ __launch_bounds__(kRdThreads) void gdn_rd_kernel(GdnArgs g) {
-  __shared__ __attribute__((aligned(16))) uint32_t Tl[256][kTs];     // block-diagonal halves of T, hi | lo
-  __shared__ __attribute__((aligned(16))) float dstage[16 * kAtBlk];  // A's diagonal blocks (A^T); then Y tiles
+__global__ __launch_bounds__(kRdThreads) void gdn_fs_kernel(GdnArgs g) {
+  // A's strictly lower blocks (b, c), block index b (b - 1) / 2 + c.  Row r16 of a block is 16
+  // words: per 4-column quarter, the operand record of the lane that reads it (bf16 hi parts of
+  // the 4 values as two pairs, then the lo parts), so an A operand is one 16-byte read with no
+  // unpacking, and a block's reads are one contiguous KiB
+  __shared__ __attribute__((aligned(16))) uint32_t Al[kFsLowBlocks][16][16];
+  __shared__ __attribute__((aligned(16))) uint32_t Td[kFsMaxNB][16][kFsTd];  // T_bb, hi | lo
+  __shared__ __attribute__((aligned(16))) float dstage[kFsMaxNB * kAtBlk];   // A_bb^T for level 0
   const int t = threadIdx.x, lane = t & 63;
-  // The wave index (and the task indexes derived from it) must be scalar: the merge loops branch
-  // on it, and a branch on a vector value becomes an exec-masked region, in which the MFMA still
-  // runs while the conversions that build its operands do not.
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  // Workgroups go to the 8 XCDs round-robin (block b on XCD b % 8), each XCD with its own L2: the
-  // `groups` workgroups of one head all read that head's A, so they are given block indexes of
-  // one residue mod 8.  Block b: XCD x = b % 8, k = b / 8, part = k % groups, head = x + 8 (k /
-  // groups); the grid is rounded up to whole sets of 8 heads.
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // scalar: strip choices branch on it
   const int k8 = blockIdx.x >> 3;
   const int head = (blockIdx.x & 7) + 8 * (k8 / g.groups), part = k8 % g.groups;
   if (head >= g.heads) return;  // uniform: the whole workgroup leaves before any barrier
   const size_t hbase = static_cast<size_t>(head) * g.C * g.C;
-  switch (g.P) {
-    case 16: {  // one diagonal block
-      if (t < 64) {
-        const int i = (lane >> 2) & 15, k4 = lane & 3;
-        stage_at(dstage, 0, i, k4, load_a4<U16>(g, hbase, i, 4 * k4));
-      }
-      lds_barrier();
-      level0<U16, SPLIT>(g, hbase, Tl, dstage, 1, 0, t);
-      store_zeros<U16>(g, hbase, 0, wave, lane);
-      break;
+  const int C = g.C, NB = C / 16;
+
+  // ---- A reads: the diagonal blocks (level 0) first, then the strictly lower blocks -------------
+  float4 dv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {  // block wave + 8 u, row (t / 4) % 16, quarter t % 4
+    const int bb = wave + 8 * u, i = (lane >> 2) & 15, k4 = lane & 3;
+    dv[u] = load_a4_or0<U16>(g, hbase, 16 * bb + i, 16 * bb + 4 * k4, bb < NB);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // level 0's reads first: its wait then covers only them
+  // lower block slot s = t + 512 u (u < 15): block s / 64 in row-major (b, c) order, row
+  // (s / 4) % 16, quarter s % 4
+  constexpr int kLowLoads = kFsLowBlocks * 64 / kRdThreads;
+  static_assert(kFsLowBlocks * 64 % kRdThreads == 0, "whole lower-block loads per thread");
+  const int nlow = NB * (NB - 1) / 2;
+  float4 lv[kLowLoads];
+#pragma unroll
+  for (int u = 0; u < kLowLoads; ++u) {
+    const int s = t + kRdThreads * u, blk = s >> 6;
+    // block index -> (b, c): b is the largest with b (b - 1) / 2 <= blk
+    int b = 1;
+#pragma unroll
+    for (int bb = 2; bb < kFsMaxNB; ++bb) b = (bb * (bb - 1) / 2 <= blk) ? bb : b;
+    const int c = blk - b * (b - 1) / 2;
+    lv[u] = load_a4_or0<U16>(g, hbase, 16 * b + ((s >> 2) & 15), 16 * c + 4 * (s & 3), blk < nlow);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- level 0 --------------------------------------------------------------------------------
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int bb = wave + 8 * u, i = (lane >> 2) & 15, k4 = lane & 3;
+    if (bb < NB) stage_at(dstage, bb, i, k4, dv[u]);
+  }
+  lds_barrier();
+  fs_level0<SPLIT>(Td, dstage, NB, t);
+#pragma unroll
+  for (int u = 0; u < kLowLoads; ++u) {
+    const int s = t + kRdThreads * u, blk = s >> 6;
+    if (blk < nlow) {
+      // the operand record of lane (row, quarter): hi pairs then lo pairs, read as one Half4
+      const Half4 h = split4<SPLIT>(lv[u]);
+      *reinterpret_cast<uint4 *>(&Al[blk][(s >> 2) & 15][fs_col((s >> 2) & 15, 4 * (s & 3))]) =
+          make_uint4(h.h01, h.h23, h.l01, h.l23);
     }
-    case 32: solve_head<U16, SPLIT, 5>(g, Tl, dstage, part, hbase, t, wave, lane); break;
-    case 64: solve_head<U16, SPLIT, 6>(g, Tl, dstage, part, hbase, t, wave, lane); break;
-    case 128: solve_head<U16, SPLIT, 7>(g, Tl, dstage, part, hbase, t, wave, lane); break;
-    default: solve_head<U16, SPLIT, 8>(g, Tl, dstage, part, hbase, t, wave, lane); break;
+  }
+  lds_barrier();
+
+  // ---- the wave's strip ---------------------------------------------------------------------------
+  const int j = __builtin_amdgcn_readfirstlane(fs_strip(NB, part, wave));
+  if (j >= 0) fs_strip_solve<U16, SPLIT>(g, hbase, Al, Td, dstage, NB, j, lane);
+  // Zeros above the diagonal blocks, after the strips and by waves 4..7 (the shorter strips):
+  // issued before the strips they held the longest strip back by about a microsecond
+  if (wave >= 4) {
+    for (int row = part + (wave - 4) * g.groups; row < C; row += 4 * g.groups) {
+      const int c = 4 * lane;
+      if (c < C && c >= 16 * (row / 16) + 16) {
+        const size_t idx = hbase + static_cast<size_t>(row) * C + c;
+        if (U16) {
+          const uint32_t zc = static_cast<uint32_t>(g.zpT) * 0x10001u;  // code of 0.0: clip(zpT)
+          *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(g.T) + idx) = make_uint2(zc, zc);
+        } else {
+          *reinterpret_cast<float4 *>(static_cast<float *>(g.T) + idx) = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
   }
 }
 
-template <bool U16, bool SPLIT>
-qh_status launch(const GdnArgs &g, int heads, hipStream_t stream) {
-  const long long blocks = static_cast<long long>((heads + 7) / 8) * 8 * g.groups;
-  if (blocks > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "gdn: %d heads exceed one launch", heads);
-  hipLaunchKernelGGL((gdn_rd_kernel<U16, SPLIT>), dim3(static_cast<unsigned>(blocks)), dim3(kRdThreads), 0, stream, g);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return hip_fail(err, "gdn_rd_kernel launch");
-  return QH_STATUS_OK;
+// G = 2 workgroups per head for more than 8 strips, one otherwise.
+GdnArgs make_args(const void *A, void *T, int heads, int C, int zpA, int zpT, float sA, float sT) {
+  return GdnArgs{A, T, C, C / 16 > 8 ? 2 : 1, heads, zpA, zpT, sA, sT, 1.0f / sT};
 }
 
-GdnArgs make_args(const void *A, void *T, int heads, int C, int zpA, int zpT, float sA, float sT) {
-  int P = 16;
-  while (P < C) P *= 2;
-  return GdnArgs{A, T, C, P, P >= 32 ? P / 2 : 16, P >= 32 ? P / 32 : 1, heads, zpA, zpT, sA, sT, 1.0f / sT};
+template <bool U16, bool SPLIT>
+qh_status launch_fs(const GdnArgs &g, int heads, hipStream_t stream) {
+  const long long blocks = static_cast<long long>((heads + 7) / 8) * 8 * g.groups;
+  if (blocks > 0x7FFFFFFFLL) return fail(QH_STATUS_SHAPE_UNSUPPORTED, "gdn: %d heads exceed one launch", heads);
+  hipLaunchKernelGGL((gdn_fs_kernel<U16, SPLIT>), dim3(static_cast<unsigned>(blocks)), dim3(kRdThreads), 0, stream, g);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "gdn_fs_kernel launch");
+  return QH_STATUS_OK;
 }
 
 }  // namespace
 
 qh_status launch_gdn_solve_f32(const float *A, float *T, int heads, int C, int precision, hipStream_t stream) {
   const GdnArgs g = make_args(A, T, heads, C, 0, 0, 1.0f, 1.0f);
-  return precision == QH_GDN_BF16 ? launch<false, false>(g, heads, stream) : launch<false, true>(g, heads, stream);
+  return precision == QH_GDN_BF16 ? launch_fs<false, false>(g, heads, stream) : launch_fs<false, true>(g, heads, stream);
 }
 
 qh_status launch_gdn_solve_u16(const uint16_t *A, uint16_t *T, int heads, int C, int zpA, int zpT, float sA, float sT,
                                int precision, hipStream_t stream) {
   const GdnArgs g = make_args(A, T, heads, C, zpA, zpT, sA, sT);
-  return precision == QH_GDN_BF16 ? launch<true, false>(g, heads, stream) : launch<true, true>(g, heads, stream);
+  return precision == QH_GDN_BF16 ? launch_fs<true, false>(g, heads, stream) : launch_fs<true, true>(g, heads, stream);
 }
 
 }  // namespace qh

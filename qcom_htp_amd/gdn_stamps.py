@@ -1,17 +1,18 @@
-"""Per-phase cycle stamps of the GDN solve kernel, and its merge-phase matrix-core utilisation.
+"""Per-phase cycle stamps of the GDN solve kernel, and its matrix-core utilisation in the strips.
 
     python -m qcom_htp_amd.gdn_stamps [--heads 32] [--C 256] [--json out.json]
 
 A profiling tool, not a product path: it writes a timing copy of ``csrc/gdn_solve.hip`` in which
 thread 0 of every workgroup records ``s_memtime`` (shader clock) at the phase boundaries of
-``solve_head`` -- A reads issued, level 0, the zero stores, the merge levels s = 16, 32, 64 inside
-the halves, and the last merge's Y and X products -- compiles it into ``_build/stamps/`` and runs
-it on the C x heads solve workload (both precisions).  It prints the median cycles of each phase over
-the workgroups and the merge window (start of s16 to the last store).
+``gdn_fs_kernel`` -- A reads issued and the diagonal blocks staged, level 0, the strictly lower
+blocks staged, the strip steps of wave 0 (the workgroup's longest strip, each storing its tile) --
+compiles it into ``_build/stamps/`` and runs it on the C x heads solve workload (both
+precisions).  It prints the median cycles of each phase over the workgroups and the strip window
+(strips start to the end of wave 0's steps).
 
 With the executed MFMA operations of the same launch (``SQ_INSTS_VALU_MFMA_MOPS_BF16`` x 512 from
 ``rocprofv3 --pmc``, passed as ``--exec-bf16-ops``/``--exec-fp32-ops``), it also prints the
-per-active-CU utilisation inside the merge window: operations per workgroup / (window cycles x
+per-active-CU utilisation inside the strip window: operations per workgroup / (window cycles x
 4096 bf16 flop per CU cycle, MI355X's 2.5 PFLOP/s at 2.4 GHz over 256 CUs).  The algorithmic
 count is the (2/3) C^3 flop of the inverse minus level 0's diagonal blocks, spread over the
 head's workgroups.
@@ -29,20 +30,22 @@ from pathlib import Path
 from . import build as B
 
 OUT = B.OBJDIR / "stamps"
-PHASES = ["A reads", "level 0", "zero stores", "s16", "s32", "s64", "last merge Y", "last merge X"]
+PHASES = ["A reads and diagonal staging", "level 0", "lower blocks staged", "strip steps (stores issued as they go)", "strip end"]
 BF16_FLOP_PER_CU_CYCLE = 2.5e15 / (256 * 2.4e9)
 
 _ANCHORS = [
-    ("  // ---- A reads", 0), ("  // ---- level 0 ---", 1), ("  store_zeros<U16>(g, hbase, part, wave, lane);\n\n", 2),
-    ("  // ---- merges inside the halves", 3), ("  if (P > 64) merge_level", 4), ("  if (P > 128) merge_level", 5),
-    ("  // ---- last merge, strip", 6), ("  lds_barrier();\n  if (wave < NBF) {\n    v4f acc", 7),
+    ("  // ---- A reads", 0),
+    ("  fs_level0<SPLIT>(Td, dstage, NB, t);\n", 1),
+    ("#pragma unroll\n  for (int u = 0; u < kLowLoads; ++u) {\n    const int s = t + kRdThreads * u, blk = s >> 6;\n    if (blk < nlow) {", 2),
+    ("  // ---- the wave's strip", 3),
+    ("#pragma unroll\n  for (int v = 0; v < kFsMaxNB; ++v)\n    if (v <= steps) asm volatile", 4),
 ]
 
 
 def stamped_source() -> str:
     """The solve source with the stamps inserted (raises if the kernel's structure changed)."""
     src = (B.CSRC / "gdn_solve.hip").read_text()
-    cut = src.index("template <bool U16, bool SPLIT>\nqh_status launch")
+    cut = src.index("// G = 2 workgroups per head for more than 8 strips, one otherwise.\nGdnArgs make_args")
     src = src[:cut] + "}  // namespace\n}  // namespace qh\n"
     src = src.replace(
         "namespace qh {\nnamespace {",
@@ -50,26 +53,23 @@ def stamped_source() -> str:
         "__shared__ unsigned long long s_ts[16];\n"
         "#define STAMP(k) do { if (threadIdx.x == 0) s_ts[(k)] = __builtin_readcyclecounter(); } while (0)\n", 1)
     for anchor, k in _ANCHORS:
-        if anchor not in src:
-            raise RuntimeError(f"gdn_solve.hip changed: anchor not found: {anchor!r}")
+        if src.count(anchor) != 1:
+            raise RuntimeError(f"gdn_solve.hip changed: anchor not found once: {anchor!r}")
         src = src.replace(anchor, f"  STAMP({k});\n" + anchor, 1)
-    last = ("    if (P / 2 + 16 * wave < C && 16 * part < C) store_tile<U16>(g, hbase, P / 2 + 16 * wave, 16 * part + r16, q, acc);\n"
-            "  }\n")
-    fin = "    default: solve_head<U16, SPLIT, 8>(g, Tl, dstage, part, hbase, t, wave, lane); break;\n  }\n"
-    if last not in src or fin not in src:
-        raise RuntimeError("gdn_solve.hip changed: end anchors not found")
-    src = src.replace(last, last + "  STAMP(8);\n", 1)
-    src = src.replace(fin, fin + "  if (threadIdx.x == 0) for (int k = 0; k < 9; ++k) g_st[(head * g.groups + part) * 16 + k] = s_ts[k];\n", 1)
+    call = "  if (j >= 0) fs_strip_solve<U16, SPLIT>(g, hbase, Al, Td, dstage, NB, j, lane);\n"
+    if src.count(call) != 1:
+        raise RuntimeError("gdn_solve.hip changed: strip call not found")
+    src = src.replace(call, call + "  STAMP(5);\n"
+                      "  if (threadIdx.x == 0) for (int k = 0; k < 6; ++k) g_st[(head * g.groups + part) * 16 + k] = s_ts[k];\n", 1)
     src += """
 extern "C" int stamps_set(unsigned long long *stamps) {
   return (int)hipMemcpyToSymbol(HIP_SYMBOL(qh::g_st), &stamps, sizeof(stamps));
 }
 extern "C" int stamps_solve(const void *A, void *T, int heads, int C, int split, void *stream) {
-  int P = 16; while (P < C) P *= 2;
-  qh::GdnArgs g{A, T, C, P, P >= 32 ? P / 2 : 16, P >= 32 ? P / 32 : 1, heads, 0, 0, 1.0f, 1.0f, 1.0f};
+  qh::GdnArgs g{A, T, C, C / 16 > 8 ? 2 : 1, heads, 0, 0, 1.0f, 1.0f, 1.0f};
   const dim3 grid((heads + 7) / 8 * 8 * g.groups);
-  if (split) hipLaunchKernelGGL((qh::gdn_rd_kernel<false, true>), grid, dim3(512), 0, (hipStream_t)stream, g);
-  else hipLaunchKernelGGL((qh::gdn_rd_kernel<false, false>), grid, dim3(512), 0, (hipStream_t)stream, g);
+  if (split) hipLaunchKernelGGL((qh::gdn_fs_kernel<false, true>), grid, dim3(512), 0, (hipStream_t)stream, g);
+  else hipLaunchKernelGGL((qh::gdn_fs_kernel<false, false>), grid, dim3(512), 0, (hipStream_t)stream, g);
   return (int)hipGetLastError();
 }
 """
@@ -111,13 +111,10 @@ def run(heads: int, C: int, exec_ops: dict) -> dict:
     lib = ctypes.CDLL(str(build_stamped()))
     lib.stamps_solve.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.stamps_set.argtypes = [ctypes.c_void_p]
-    P = 16
-    while P < C:
-        P *= 2
-    G = P // 32 if P >= 32 else 1
+    G = 2 if C // 16 > 8 else 1
     A = torch.from_numpy(config4_A(heads, C)).cuda()
     T = torch.empty_like(A)
-    st = torch.zeros(heads * G * 16, dtype=torch.int64, device="cuda")
+    st = torch.zeros(((heads + 7) // 8 * 8) * G * 16, dtype=torch.int64, device="cuda")
     if lib.stamps_set(st.data_ptr()) != 0:
         raise RuntimeError("stamps_set failed")
     alg_wg = ((2.0 / 3.0) * C ** 3 - (C // 16) * (2.0 / 3.0) * 16 ** 3) / G
@@ -127,23 +124,23 @@ def run(heads: int, C: int, exec_ops: dict) -> dict:
             if lib.stamps_solve(A.data_ptr(), T.data_ptr(), heads, C, split, torch.cuda.current_stream().cuda_stream) != 0:
                 raise RuntimeError("stamps_solve failed")
         torch.cuda.synchronize()
-        s = st.view(heads * G, 16).cpu().numpy().astype(np.int64)[:, :9]
+        s = st.view(-1, 16).cpu().numpy().astype(np.int64)[: heads * G, :6]
         d = np.diff(s, axis=1)
-        window = s[:, 8] - s[:, 3]
-        r = {"phase_cycles_median": {PHASES[i]: float(np.median(d[:, i])) for i in range(8)},
-             "merge_window_cycles_median": float(np.median(window)), "merge_window_cycles_mean": float(window.mean()),
-             "workgroup_cycles_median": float(np.median(s[:, 8] - s[:, 0])), "workgroups": int(len(s)),
-             "algorithmic_merge_flop_per_workgroup": alg_wg,
-             "algorithmic_merge_utilisation": alg_wg / (window.mean() * BF16_FLOP_PER_CU_CYCLE)}
+        window = s[:, 4] - s[:, 3]
+        r = {"phase_cycles_median": {PHASES[i]: float(np.median(d[:, i])) for i in range(5)},
+             "strip_window_cycles_median": float(np.median(window)), "strip_window_cycles_mean": float(window.mean()),
+             "workgroup_cycles_median": float(np.median(s[:, 5] - s[:, 0])), "workgroups": int(len(s)),
+             "algorithmic_flop_per_workgroup": alg_wg,
+             "algorithmic_strip_utilisation": alg_wg / (window.mean() * BF16_FLOP_PER_CU_CYCLE)}
         if exec_ops.get(name):
             ops_wg = exec_ops[name] / (heads * G)
             r["executed_ops_per_workgroup"] = ops_wg
-            r["executed_merge_utilisation"] = ops_wg / (window.mean() * BF16_FLOP_PER_CU_CYCLE)
+            r["executed_strip_utilisation"] = ops_wg / (window.mean() * BF16_FLOP_PER_CU_CYCLE)
         res[name] = r
         print(f"{name}: " + ", ".join(f"{p} {v:.0f}" for p, v in r["phase_cycles_median"].items()) +
-              f"; merge window {r['merge_window_cycles_median']:.0f} cycles (median of {len(s)} workgroups); "
-              f"algorithmic merge utilisation {100 * r['algorithmic_merge_utilisation']:.2f}%" +
-              (f", executed {100 * r['executed_merge_utilisation']:.2f}%" if "executed_merge_utilisation" in r else ""),
+              f"; strip window {r['strip_window_cycles_median']:.0f} cycles (median of {len(s)} workgroups); "
+              f"algorithmic strip utilisation {100 * r['algorithmic_strip_utilisation']:.2f}%" +
+              (f", executed {100 * r['executed_strip_utilisation']:.2f}%" if "executed_strip_utilisation" in r else ""),
               flush=True)
     return res
 
@@ -152,8 +149,8 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--C", type=int, default=256)
-    ap.add_argument("--exec-bf16-ops", type=float, default=0.0, help="executed MFMA ops per launch, bf16 merges")
-    ap.add_argument("--exec-fp32-ops", type=float, default=0.0, help="executed MFMA ops per launch, fp32 (hi/lo) merges")
+    ap.add_argument("--exec-bf16-ops", type=float, default=0.0, help="executed MFMA ops per launch, bf16 products")
+    ap.add_argument("--exec-fp32-ops", type=float, default=0.0, help="executed MFMA ops per launch, fp32 (hi/lo) products")
     ap.add_argument("--json", default="")
     a = ap.parse_args()
     sys.path.insert(0, str(B.ROOT))
