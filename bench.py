@@ -231,7 +231,9 @@ def gdn_workload(heads: int, C: int, steps: int, warmup: int, precision: int):
     launch = lambda i: gdn_solve(a, precision=precision, out=out)
     wall, ev = time_graph(launch, steps, warmup)  # a solve is about as short as its launch from Python
     wall_e, ev_e = time_kernel(launch, steps, 0)
-    flops = (2.0 / 3.0) * C ** 3 * heads
+    # the inverse of a unit lower-triangular C x C matrix: sum_j sum_{i>j} (i - j) multiply-adds
+    # = C^3 / 6, i.e. C^3 / 3 flop
+    flops = C ** 3 / 3.0 * heads
     from oracle import gdn as og  # the checker
 
     err = og.oc(out.cpu().numpy(), og.inverse_fp64(A))
@@ -259,8 +261,8 @@ def gdn_chunk_workload(B: int, T: int, H: int, C: int, steps: int, warmup: int):
     gc = torch.nn.functional.logsigmoid(torch.randn((B, T, H), generator=gen, device=dev) + 3.0)
     wall, ev = time_kernel(lambda i: gdn_chunk_uw(k, v, gc, beta, C), steps, warmup)
     chunk_heads = B * (T // C) * H
-    # dense algorithmic work per chunk-head: A = K K^T (2 C^2 D), inverse (2/3 C^3), W and U (2 C^2 D each)
-    flops = chunk_heads * (3 * 2.0 * C * C * D + (2.0 / 3.0) * C ** 3)
+    # dense algorithmic work per chunk-head: A = K K^T (2 C^2 D), inverse (C^3 / 3), W and U (2 C^2 D each)
+    flops = chunk_heads * (3 * 2.0 * C * C * D + C ** 3 / 3.0)
     nbytes = B * T * H * (4 * D * 2 + 2 * 4)  # K, V in + W, U out (bf16) + beta, g (fp32)
     # after the timed region: the outputs of a sample of (batch, chunk, head) items, first and
     # last included, against the float64 solve
@@ -411,7 +413,7 @@ def gdn_u16_workload(heads: int, C: int, steps: int, warmup: int, precision: int
     err = og.oc(Td, og.inverse_fp64(Ad))
     if not err <= og.GATE_BF16:
         raise RuntimeError(f"GDN u16 C={C}: oc {err:.3e} > {og.GATE_BF16}")
-    flops = (2.0 / 3.0) * C ** 3 * heads
+    flops = C ** 3 / 3.0 * heads  # the inverse's C^3 / 3 flop per head
     return {"heads": heads, "C": C, "precision": "fp32" if precision == 0 else "bf16", "ms": ev, "wall_ms": wall,
             "heads_per_s": heads / (ev * 1e-3), "tflops_alg": flops / (ev * 1e-3) / 1e12, "oc_vs_fp64": err,
             "eager_ms": ev_e, "sA": sA, "sT": sT, "zp": 32768}

@@ -14,8 +14,8 @@ With the executed MFMA operations of the same launch (``SQ_INSTS_VALU_MFMA_MOPS_
 ``rocprofv3 --pmc``, passed as ``--exec-bf16-ops``/``--exec-fp32-ops``), it also prints the
 per-active-CU utilisation inside the strip window: operations per workgroup / (window cycles x
 4096 bf16 flop per CU cycle, MI355X's 2.5 PFLOP/s at 2.4 GHz over 256 CUs).  The algorithmic
-count is the (2/3) C^3 flop of the inverse minus level 0's diagonal blocks, spread over the
-head's workgroups.
+count is the C^3 / 3 flop of the unit lower-triangular inverse (C^3 / 6 multiply-adds) minus level
+0's diagonal blocks, spread over the head's workgroups.
 """
 
 from __future__ import annotations
@@ -117,7 +117,7 @@ def run(heads: int, C: int, exec_ops: dict) -> dict:
     st = torch.zeros(((heads + 7) // 8 * 8) * G * 16, dtype=torch.int64, device="cuda")
     if lib.stamps_set(st.data_ptr()) != 0:
         raise RuntimeError("stamps_set failed")
-    alg_wg = ((2.0 / 3.0) * C ** 3 - (C // 16) * (2.0 / 3.0) * 16 ** 3) / G
+    alg_wg = (C ** 3 / 3.0 - (C // 16) * 16 ** 3 / 3.0) / G
     res = {}
     for split, name in ((0, "bf16"), (1, "fp32")):
         for _ in range(5):
