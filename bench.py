@@ -184,7 +184,10 @@ def gemv_workload(family: str, m: int, k: int, n: int, steps: int, warmup: int, 
     nbytes = info["gemv_weight_bytes"] + per_ch + act_b + out_b
     res = {"family": family, "m": m, "k": k, "n": n, "ms": ev, "wall_ms": wall, "bytes": nbytes,
            "gbs": nbytes / (ev * 1e-3) / 1e9, "weight_copies": copies,
-           "rotated_mb": copies * info["gemv_weight_bytes"] / 1e6, **check}
+           "rotated_mb": copies * info["gemv_weight_bytes"] / 1e6,
+           # device memory the prepared weight state holds (GEMM tiles, GEMV stream, residue plane,
+           # per-channel constants), as qh_qmm_query reports it
+           "prepared_state_mb": info["device_bytes"] / 1e6, **check}
     for o in ops:
         o.close()
     return res
